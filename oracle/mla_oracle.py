@@ -1,0 +1,205 @@
+"""CPU oracle for the weight-absorbed MLA decode path.
+
+TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg may import this module, and only as the
+checker (or the timed CPU baseline). The product path (``ada_mla``) never
+imports it and fails loudly when its HIP library is missing.
+
+Contents, each restating a reference function:
+
+``closed_form``          mla_decode_torch (mla.py:44-47):
+                         softmax(q @ c.T / sqrt(192)) @ c[:, :512], in float64.
+``sdpa_math``            mla_decode_sdpa with the MATH backend (mla.py:49-66):
+                         key = c, value = c[:, :512], scale 1/sqrt(192); the
+                         math backend scales q and k by sqrt(scale) each before
+                         the product, restated the same way.
+``closed_form_batched``  the batched decode (no reference counterpart: the
+                         reference has no batch dimension, csrc/mla_api.cpp:67-69)
+                         = closed_form applied per sequence of a packed cache.
+``split_partials`` /
+``lse_merge``            the split-KV partial results and the combine of
+                         mla_decode_combine (csrc/mla_decode_splitk_fwd.cuh:894-939),
+                         in float64 with the running max started at -inf
+                         instead of the smallest fp16 denormal.
+``naive_cpu``            ctypes binding of oracle/mla_naive_cpu.c, the C
+                         restatement of run_mla_decode_cpu
+                         (csrc/mla_decode_naive_fp32_cpu.cpp:5-61).
+``reference_cpu``        ctypes binding of the reference's own run_mla_decode_cpu,
+                         compiled from its source into oracle/_ref by
+                         oracle/Makefile (absent where /root/reference was not).
+
+Pinning (tests/test_oracle.py): ``naive_cpu`` in the reference's own form is
+bit-identical to ``reference_cpu`` and to the committed golden vectors
+written by it; ``closed_form`` agrees with the reference kernel through the
+exact identity 1/sqrt(192) = sqrt(3)/sqrt(576); the closed form is checked
+against textbook special cases (N = 1, equal rows, q = 0, a dominant logit,
+token permutation, brute force on tiny shapes); ``lse_merge`` against the
+unsplit closed form for every split point on small inputs.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+import numpy as np
+
+HEAD_DIM_C = 512   # mla.py:31
+HEAD_DIM_ROPE = 64  # mla.py:32
+HEAD_DIM_K = HEAD_DIM_C + HEAD_DIM_ROPE  # mla.py:33 (576)
+HEAD_DIM = 128     # mla.py:30; the softmax scale uses HEAD_DIM + HEAD_DIM_ROPE
+SCALE = 1.0 / math.sqrt(HEAD_DIM + HEAD_DIM_ROPE)  # mla.py:46: 1/sqrt(192)
+REF_CPU_DIVISOR = math.sqrt(HEAD_DIM_K)            # cpu.cpp:24: sqrt(576)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_ORACLE_LIB = os.path.join(_HERE, "liboracle_mla.so")
+_REF_LIB = os.path.join(_HERE, "_ref", "libref_mla_cpu.so")
+
+
+def _softmax_rows(x: np.ndarray) -> np.ndarray:
+    m = x.max(axis=-1, keepdims=True)
+    e = np.exp(x - m)
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def closed_form(q, c, scale: float = SCALE, dv: int = HEAD_DIM_C) -> np.ndarray:
+    """softmax(scale * q c^T) c[:, :dv] in float64 (mla.py:44-47)."""
+    q = np.asarray(q, dtype=np.float64)
+    c = np.asarray(c, dtype=np.float64)
+    if q.ndim != 2 or c.ndim != 2 or q.shape[1] != c.shape[1] or c.shape[0] < 1:
+        raise ValueError("closed_form: q [n_h, d], c [N>=1, d] expected")
+    p = _softmax_rows((q @ c.T) * scale)
+    return p @ c[:, :dv]
+
+
+def sdpa_math(q, c, scale: float = SCALE, dv: int = HEAD_DIM_C) -> np.ndarray:
+    """SDPA math-backend form of mla.py:49-62 (key = c, value = c[:, :512]):
+    q and k are each multiplied by sqrt(scale) before the product."""
+    q = np.asarray(q, dtype=np.float64)
+    c = np.asarray(c, dtype=np.float64)
+    s = math.sqrt(scale)
+    p = _softmax_rows((q * s) @ (c * s).T)
+    return p @ c[:, :dv]
+
+
+def closed_form_batched(q, c_packed, cu_seqlens, scale: float = SCALE,
+                        dv: int = HEAD_DIM_C) -> np.ndarray:
+    """Per-sequence closed form over a packed cache: q [B, n_h, d], c_packed
+    [sum N_b, d], cu_seqlens [B + 1]. An empty sequence yields zeros."""
+    q = np.asarray(q, dtype=np.float64)
+    c_packed = np.asarray(c_packed, dtype=np.float64)
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    B = q.shape[0]
+    out = np.zeros((B, q.shape[1], dv), dtype=np.float64)
+    for b in range(B):
+        lo, hi = int(cu[b]), int(cu[b + 1])
+        if hi > lo:
+            out[b] = closed_form(q[b], c_packed[lo:hi], scale, dv)
+    return out
+
+
+def split_partials(q, c, bounds, scale: float = SCALE, dv: int = HEAD_DIM_C):
+    """Unnormalised per-split results (O_s, m_s, l_s) for token ranges
+    [bounds[s], bounds[s+1]): m_s = max logit, l_s = sum exp(logit - m_s),
+    O_s = sum exp(logit - m_s) c[:, :dv]. This is what each split CTA of
+    mla_decode_splitk_mma_fp16 stores (csrc/mla_decode_splitk_fwd.cuh:880-891),
+    here in float64 with natural-log units."""
+    q = np.asarray(q, dtype=np.float64)
+    c = np.asarray(c, dtype=np.float64)
+    outs, ms, ls = [], [], []
+    for s in range(len(bounds) - 1):
+        lo, hi = bounds[s], bounds[s + 1]
+        if hi <= lo:
+            outs.append(np.zeros((q.shape[0], dv)))
+            ms.append(np.full(q.shape[0], -np.inf))
+            ls.append(np.zeros(q.shape[0]))
+            continue
+        logits = (q @ c[lo:hi].T) * scale
+        m = logits.max(axis=1)
+        e = np.exp(logits - m[:, None])
+        outs.append(e @ c[lo:hi, :dv])
+        ms.append(m)
+        ls.append(e.sum(axis=1))
+    return np.stack(outs), np.stack(ms), np.stack(ls)
+
+
+def lse_merge(o_parts, m_parts, l_parts) -> np.ndarray:
+    """Combine of mla_decode_combine (csrc/mla_decode_splitk_fwd.cuh:894-939):
+    m = max_s m_s; l = sum_s l_s e^(m_s - m); O = sum_s O_s e^(m_s - m) / l.
+    The running max starts at -inf (the reference starts at the smallest fp16
+    denormal, :916); splits with m_s = -inf (no tokens) contribute nothing."""
+    o_parts = np.asarray(o_parts, dtype=np.float64)
+    m_parts = np.asarray(m_parts, dtype=np.float64)
+    l_parts = np.asarray(l_parts, dtype=np.float64)
+    m = np.max(m_parts, axis=0)
+    w = np.where(np.isneginf(m_parts), 0.0, np.exp(m_parts - m[None, :]))
+    l = (l_parts * w).sum(axis=0)
+    o = (o_parts * w[:, :, None]).sum(axis=0)
+    return o / l[:, None]
+
+
+def _load(path: str):
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    return lib
+
+
+_oracle_lib = None
+
+
+def naive_cpu(q, c, divisor: float = 1.0 / SCALE, dv: int = HEAD_DIM_C) -> np.ndarray:
+    """C restatement of run_mla_decode_cpu (cpu.cpp:5-61) on float32 inputs.
+    divisor = sqrt(576), dv = 576 is the reference's own form; the default is
+    the decode contract (1/scale = sqrt(192), dv = 512)."""
+    global _oracle_lib
+    if _oracle_lib is None:
+        _oracle_lib = _load(_ORACLE_LIB)
+        if _oracle_lib is None:
+            raise RuntimeError(f"{_ORACLE_LIB} not built (run make -C oracle)")
+        f = _oracle_lib.oracle_mla_decode_cpu
+        f.restype = ctypes.c_int
+        f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                      ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                      ctypes.c_double]
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    c = np.ascontiguousarray(c, dtype=np.float32)
+    n_h, d = q.shape
+    n = c.shape[0]
+    if c.shape[1] != d or dv > d:
+        raise ValueError("naive_cpu: shape mismatch")
+    out = np.empty((n_h, dv), dtype=np.float32)
+    rc = _oracle_lib.oracle_mla_decode_cpu(q.ctypes.data, c.ctypes.data,
+                                           out.ctypes.data, n_h, d, n, dv,
+                                           float(divisor))
+    if rc != 0:
+        raise RuntimeError(f"oracle_mla_decode_cpu failed: {rc}")
+    return out
+
+
+_ref_lib = None
+
+
+def reference_cpu_available() -> bool:
+    return os.path.exists(_REF_LIB)
+
+
+def reference_cpu(q, c) -> np.ndarray:
+    """The reference's own run_mla_decode_cpu (scale 1/sqrt(576), all 576
+    output columns), compiled from its source into oracle/_ref."""
+    global _ref_lib
+    if _ref_lib is None:
+        _ref_lib = _load(_REF_LIB)
+        if _ref_lib is None:
+            raise RuntimeError(f"{_REF_LIB} not built (make -C oracle ref)")
+        f = _ref_lib.ref_run_mla_decode_cpu
+        f.restype = None
+        f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                      ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    c = np.ascontiguousarray(c, dtype=np.float32)
+    n_h, d = q.shape
+    out = np.empty((n_h, d), dtype=np.float32)
+    _ref_lib.ref_run_mla_decode_cpu(q.ctypes.data, c.ctypes.data,
+                                    out.ctypes.data, n_h, d, c.shape[0])
+    return out
