@@ -1,0 +1,145 @@
+"""ctypes binding of the C ABI in include/mla_mi355x.h (libmla_mi355x.so).
+
+This is the binding a Python caller without the torch extension would add;
+the parity tests call the kernels through it. torch is used only for device
+memory and the current stream: tensors are passed as raw device pointers.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmla_mi355x.so")
+HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(_HERE)), "include", "mla_mi355x.h")
+
+HEAD_DIM_K = 576
+HEAD_DIM_V = 512
+STATUS_SUCCESS = 0
+STATUS_INVALID_VALUE = 1
+STATUS_MISALIGNED = 2
+STATUS_WORKSPACE_TOO_SMALL = 3
+STATUS_HIP_ERROR = 4
+FLAG_SCALAR_TRANSPOSE = 1
+
+_vp, _i, _u, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint, ctypes.c_size_t
+_SIGNATURES = {
+    "mla_abi_version": (_i, []),
+    "mla_status_string": (ctypes.c_char_p, [_i]),
+    "mla_last_hip_error": (_i, []),
+    "mla_decode_split_workspace_size": (_sz, [_i, _i, _i]),
+    "mla_decode_split_fp16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
+    "mla_decode_split_fp16_ex": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _u, _vp]),
+    "mla_decode_split_fp16_partials": (_i, [_vp, _vp, _vp, _sz, _i, _i, _i, _u, _vp]),
+    "mla_decode_split_fp16_combine": (_i, [_vp, _sz, _vp, _i, _i, _i, _vp]),
+    "mla_decode_fused_workspace_size": (_sz, [_i, _i, _i]),
+    "mla_decode_fused_fp32": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+    "mla_decode_split_batched_workspace_size": (_sz, [_i, _i, _i, _i]),
+    "mla_decode_split_batched_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+}
+
+_lib = None
+
+
+class MlaError(RuntimeError):
+    def __init__(self, fn: str, status: int):
+        lib = load()
+        msg = lib.mla_status_string(status).decode()
+        if status == STATUS_HIP_ERROR:
+            msg += f" (hipError_t {lib.mla_last_hip_error()})"
+        super().__init__(f"{fn}: {msg}")
+        self.status = status
+
+
+def load():
+    """Load libmla_mi355x.so (after torch, so that the library binds to the
+    HIP runtime torch already loaded). Raises if the library is not built."""
+    global _lib
+    if _lib is None:
+        import torch  # noqa: F401
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built (run python ada-mla_amd/build.py)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            f = getattr(lib, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def declared_functions() -> list[str]:
+    """Function names declared in include/mla_mi355x.h."""
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mla_[a-z0-9_]+)\s*\(", text)))
+
+
+def _stream(t):
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _check(fn: str, st: int):
+    if st != STATUS_SUCCESS:
+        raise MlaError(fn, st)
+
+
+def decode_split_fp16(q, c, num_splits: int = 0, flags: int = 0, out=None):
+    """fp16 decode through mla_decode_split_fp16_ex: q [n_h, 576], c [N, 576]."""
+    import torch
+    lib = load()
+    assert q.dtype == torch.float16 and c.dtype == torch.float16
+    assert q.is_contiguous() and c.is_contiguous() and q.shape[1] == HEAD_DIM_K and c.shape[1] == HEAD_DIM_K
+    n_h, n = q.shape[0], c.shape[0]
+    if out is None:
+        out = torch.empty((n_h, HEAD_DIM_V), dtype=torch.float16, device=q.device)
+    ws_bytes = lib.mla_decode_split_workspace_size(n_h, n, num_splits)
+    if ws_bytes == 0:
+        raise MlaError("mla_decode_split_workspace_size", STATUS_INVALID_VALUE)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    _check("mla_decode_split_fp16_ex",
+           lib.mla_decode_split_fp16_ex(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                        ws_bytes, n_h, n, num_splits, flags, _stream(q)))
+    return out
+
+
+def decode_fused_fp32(q, c, num_splits: int = 0, out=None):
+    """fp32 decode through mla_decode_fused_fp32."""
+    import torch
+    lib = load()
+    assert q.dtype == torch.float32 and c.dtype == torch.float32
+    assert q.is_contiguous() and c.is_contiguous()
+    n_h, n = q.shape[0], c.shape[0]
+    if out is None:
+        out = torch.empty((n_h, HEAD_DIM_V), dtype=torch.float32, device=q.device)
+    ws_bytes = lib.mla_decode_fused_workspace_size(n_h, n, num_splits)
+    if ws_bytes == 0:
+        raise MlaError("mla_decode_fused_workspace_size", STATUS_INVALID_VALUE)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    _check("mla_decode_fused_fp32",
+           lib.mla_decode_fused_fp32(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                                     n_h, q.shape[1], n, num_splits, _stream(q)))
+    return out
+
+
+def decode_split_batched_fp16(q, c, cu_seqlens, num_splits: int = 0, out=None):
+    """Batched fp16 decode: q [B, n_h, 576], c [sum N, 576], cu_seqlens [B+1] int32 (device)."""
+    import torch
+    lib = load()
+    assert q.dtype == torch.float16 and c.dtype == torch.float16 and cu_seqlens.dtype == torch.int32
+    assert q.is_contiguous() and c.is_contiguous() and cu_seqlens.is_contiguous()
+    b, n_h = q.shape[0], q.shape[1]
+    total = c.shape[0]
+    if out is None:
+        out = torch.empty((b, n_h, HEAD_DIM_V), dtype=torch.float16, device=q.device)
+    ws_bytes = lib.mla_decode_split_batched_workspace_size(b, n_h, total, num_splits)
+    if ws_bytes == 0:
+        raise MlaError("mla_decode_split_batched_workspace_size", STATUS_INVALID_VALUE)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    _check("mla_decode_split_batched_fp16",
+           lib.mla_decode_split_batched_fp16(q.data_ptr(), c.data_ptr() if total else None,
+                                             cu_seqlens.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                                             b, n_h, total, num_splits, _stream(q)))
+    return out

@@ -1,0 +1,168 @@
+// PyTorch extension `ada_mla._C`: the Python surface of the reference's
+// extension module `ada_mla` (csrc/mla_api.cpp:115-120), with the same
+// function names and (query, cache) -> out contract, implemented over the
+// C ABI in include/mla_mi355x.h.
+//
+// Differences from the reference, all on inputs it mishandled:
+//  * inputs are validated (device, dtype, rank, 576 columns, num_heads a
+//    multiple of 16, N >= 1) and made contiguous; errors raise instead of
+//    being printf'd (reference TODOs csrc/mla_api.cpp:8, :18, :91).
+//  * kernels run on torch's current HIP stream of the input's device, not
+//    the legacy default stream.
+//  * mla_decode_split accepts fp32 as well (the reference's fp32 split
+//    launcher is an empty stub, csrc/mla_decode_splitk_fwd_sm89.cu:8-24, and
+//    returned uninitialised memory); mla_decode_fused accepts fp16 as well
+//    (the reference read any dtype as float*, csrc/mla_api.cpp:46-48).
+//  * an optional num_splits keyword (default: chosen from N and the CU count).
+#include <torch/extension.h>
+
+#include <c10/hip/HIPStream.h>
+
+#include "mla_mi355x.h"
+
+namespace {
+
+void check_status(int st, const char *fn)
+{
+    TORCH_CHECK(st == MLA_STATUS_SUCCESS, fn, ": ", mla_status_string(st),
+                st == MLA_STATUS_HIP_ERROR ? " (hipError_t " + std::to_string(mla_last_hip_error()) + ")"
+                                           : std::string());
+}
+
+// Shape and dtype are checked before the device so that every argument error
+// is reported the same way whatever the tensors' device.
+void check_pair(const at::Tensor &query, const at::Tensor &cache, const char *fn)
+{
+    TORCH_CHECK(query.scalar_type() == cache.scalar_type(), fn, ": query and cache must have the same dtype");
+    TORCH_CHECK(query.scalar_type() == at::kHalf || query.scalar_type() == at::kFloat, fn,
+                ": dtype must be float16 or float32, got ", query.scalar_type());
+    TORCH_CHECK(cache.dim() == 2 && cache.size(1) == MLA_HEAD_DIM_K, fn, ": cache must be [N, ",
+                MLA_HEAD_DIM_K, "], got ", cache.sizes());
+    TORCH_CHECK(cache.size(0) >= 1, fn, ": cache must hold at least one token");
+    TORCH_CHECK(cache.size(0) <= INT32_MAX, fn, ": too many tokens");
+    TORCH_CHECK(query.dim() == 2 && query.size(1) == MLA_HEAD_DIM_K, fn,
+                ": query must be [num_heads, ", MLA_HEAD_DIM_K, "], got ", query.sizes());
+    TORCH_CHECK(query.size(0) > 0 && query.size(0) % 16 == 0 && query.size(0) <= 4096, fn,
+                ": num_heads must be a positive multiple of 16 (<= 4096), got ", query.size(0));
+    TORCH_CHECK(query.is_cuda() && cache.is_cuda(), fn, ": query and cache must be GPU tensors");
+    TORCH_CHECK(query.device() == cache.device(), fn, ": query and cache must be on the same device");
+}
+
+void check_heads(int64_t num_heads, const char *fn)
+{
+    TORCH_CHECK(num_heads > 0 && num_heads % 16 == 0 && num_heads <= 4096, fn,
+                ": num_heads must be a positive multiple of 16 (<= 4096), got ", num_heads);
+}
+
+void *stream_of(const at::Tensor &t)
+{
+    return static_cast<void *>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+at::Tensor workspace(size_t bytes, const at::Tensor &like)
+{
+    return at::empty({static_cast<int64_t>(bytes)}, like.options().dtype(at::kByte));
+}
+
+// Single sequence, dispatch on dtype.
+at::Tensor decode_single(const at::Tensor &query_in, const at::Tensor &cache_in, int64_t num_splits,
+                         const char *fn)
+{
+    check_pair(query_in, cache_in, fn);
+    const at::OptionalDeviceGuard guard(query_in.device());
+    const at::Tensor query = query_in.contiguous();
+    const at::Tensor cache = cache_in.contiguous();
+    const int nh = static_cast<int>(query.size(0));
+    const int n = static_cast<int>(cache.size(0));
+    const int splits = static_cast<int>(num_splits);
+    at::Tensor out = at::empty({nh, MLA_HEAD_DIM_V}, query.options());
+    int st;
+    if (query.scalar_type() == at::kHalf) {
+        const size_t ws_bytes = mla_decode_split_workspace_size(nh, n, splits);
+        TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
+        at::Tensor ws = workspace(ws_bytes, query);
+        st = mla_decode_split_fp16(query.data_ptr(), cache.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                   ws_bytes, nh, n, splits, stream_of(query));
+    } else {
+        const size_t ws_bytes = mla_decode_fused_workspace_size(nh, n, splits);
+        TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
+        at::Tensor ws = workspace(ws_bytes, query);
+        st = mla_decode_fused_fp32(query.data_ptr<float>(), cache.data_ptr<float>(), out.data_ptr<float>(),
+                                   ws.data_ptr(), ws_bytes, nh, MLA_HEAD_DIM_K, n, splits,
+                                   stream_of(query));
+    }
+    check_status(st, fn);
+    return out;
+}
+
+// Reference: mla_decode_split (csrc/mla_api.cpp:86-113), the fp16 `-k fused`
+// path of mla.py (mla.py:177-179).
+at::Tensor mla_decode_split(const at::Tensor &query, const at::Tensor &cache, int64_t num_splits)
+{
+    return decode_single(query, cache, num_splits, "mla_decode_split");
+}
+
+// Reference: mla_decode_fused (csrc/mla_api.cpp:34-54), the `-k fused --fp32`
+// path of mla.py (mla.py:174-176).
+at::Tensor mla_decode_fused(const at::Tensor &query, const at::Tensor &cache, int64_t num_splits)
+{
+    return decode_single(query, cache, num_splits, "mla_decode_fused");
+}
+
+// No reference counterpart: B independent sequences packed back to back.
+at::Tensor mla_decode_split_batched(const at::Tensor &query_in, const at::Tensor &cache_in,
+                                    const at::Tensor &cu_seqlens_in, int64_t num_splits)
+{
+    const char *fn = "mla_decode_split_batched";
+    TORCH_CHECK(query_in.scalar_type() == at::kHalf && cache_in.scalar_type() == at::kHalf, fn,
+                ": query and cache must be float16");
+    TORCH_CHECK(cu_seqlens_in.scalar_type() == at::kInt && cu_seqlens_in.dim() == 1, fn,
+                ": cu_seqlens must be a 1-D int32 tensor");
+    TORCH_CHECK(query_in.dim() == 3 && query_in.size(2) == MLA_HEAD_DIM_K, fn,
+                ": query must be [batch, num_heads, ", MLA_HEAD_DIM_K, "], got ", query_in.sizes());
+    TORCH_CHECK(cache_in.dim() == 2 && cache_in.size(1) == MLA_HEAD_DIM_K, fn, ": cache must be [total, ",
+                MLA_HEAD_DIM_K, "], got ", cache_in.sizes());
+    TORCH_CHECK(query_in.size(0) >= 1 && cu_seqlens_in.size(0) == query_in.size(0) + 1, fn,
+                ": cu_seqlens must have batch + 1 entries");
+    TORCH_CHECK(cache_in.size(0) <= INT32_MAX, fn, ": too many tokens");
+    check_heads(query_in.size(1), fn);
+    TORCH_CHECK(query_in.is_cuda() && cache_in.is_cuda() && cu_seqlens_in.is_cuda(), fn,
+                ": query, cache and cu_seqlens must be GPU tensors");
+    TORCH_CHECK(query_in.device() == cache_in.device() && query_in.device() == cu_seqlens_in.device(), fn,
+                ": all inputs must be on the same device");
+    const at::OptionalDeviceGuard guard(query_in.device());
+    const at::Tensor query = query_in.contiguous();
+    const at::Tensor cache = cache_in.contiguous();
+    const at::Tensor cu = cu_seqlens_in.contiguous();
+    const int batch = static_cast<int>(query.size(0));
+    const int nh = static_cast<int>(query.size(1));
+    const int total = static_cast<int>(cache.size(0));
+    const int splits = static_cast<int>(num_splits);
+    at::Tensor out = at::empty({batch, nh, MLA_HEAD_DIM_V}, query.options());
+    const size_t ws_bytes = mla_decode_split_batched_workspace_size(batch, nh, total, splits);
+    TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
+    at::Tensor ws = workspace(ws_bytes, query);
+    const int st = mla_decode_split_batched_fp16(query.data_ptr(), total > 0 ? cache.data_ptr() : nullptr,
+                                                 cu.data_ptr<int>(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                                                 batch, nh, total, splits, stream_of(query));
+    check_status(st, fn);
+    return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
+{
+    m.doc() = "MI355X (gfx950) MLA decode: drop-in for the ada_mla extension's fused path";
+    m.def("mla_decode_split", &mla_decode_split, "fp16 split-KV MLA decode (query [n_h,576], cache [N,576])",
+          pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("num_splits") = 0);
+    m.def("mla_decode_fused", &mla_decode_fused, "fp32 MLA decode (query [n_h,576], cache [N,576])",
+          pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("num_splits") = 0);
+    m.def("mla_decode_split_batched", &mla_decode_split_batched,
+          "batched fp16 MLA decode (query [B,n_h,576], packed cache [sum N,576], cu_seqlens [B+1] int32)",
+          pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("cu_seqlens"),
+          pybind11::arg("num_splits") = 0);
+    m.attr("HEAD_DIM_C") = MLA_HEAD_DIM_V;
+    m.attr("HEAD_DIM_ROPE") = MLA_HEAD_DIM_K - MLA_HEAD_DIM_V;
+    m.attr("HEAD_DIM_K") = MLA_HEAD_DIM_K;
+}

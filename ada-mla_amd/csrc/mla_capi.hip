@@ -1,0 +1,282 @@
+// C ABI of the MLA decode library (declared in include/mla_mi355x.h):
+// argument validation, split planning, workspace carving and the two
+// launches (split kernel, then combine) on the caller's stream.
+#include "mla_mi355x.h"
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdint>
+
+#include "mla_internal.hpp"
+
+namespace mla {
+namespace {
+
+thread_local int t_last_hip_error = 0;
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+
+// CUs of the current device (cached); 256 (MI355X) if it cannot be queried.
+int current_cu_count()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return 256;
+    int n = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (n > 0)
+        return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = 256;
+    g_cu_count[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Smallest token count worth a split of its own: below this the fp32
+// partial write-back ([num_heads x 512] floats per split) outweighs the C
+// bytes the split reads.
+constexpr int kMinSplitTokensF16 = 256;
+constexpr int kMinSplitTokensF32 = 64;
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+float scale_log2()
+{
+    // softmax scale 1/sqrt(192) (mla.py:46) folded with log2(e): the kernels
+    // exponentiate with exp2.
+    return (float)(1.4426950408889634 / std::sqrt(192.0));
+}
+
+int fail_hip(hipError_t e)
+{
+    t_last_hip_error = (int)e;
+    return MLA_STATUS_HIP_ERROR;
+}
+
+}  // namespace
+
+Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
+               int num_splits, int cu_count)
+{
+    Plan p{};
+    if (fp32) {
+        p.head_tile = 16;
+        p.block_tokens = 16;
+    } else {
+        p.head_tile = (num_heads % 32 == 0) ? 32 : 16;
+        p.block_tokens = (p.head_tile == 32) ? 32 : 64;
+    }
+    p.n_head_tiles = num_heads / p.head_tile;
+    const int wgs_per_cu = (!fp32 && p.head_tile == 32) ? 2 : 1;
+    if (total_tokens <= 0) {
+        p.chunk = p.block_tokens;
+        p.n_chunks = 0;
+        p.n_slots = batch;  // unused; keeps the workspace non-empty
+        p.xcd_remap = 0;
+        return p;
+    }
+    int w;
+    if (num_splits > 0) {
+        w = num_splits;
+    } else {
+        w = (cu_count * wgs_per_cu) / p.n_head_tiles;
+        const int min_tok = fp32 ? kMinSplitTokensF32 : kMinSplitTokensF16;
+        w = std::min(w, ceil_div(total_tokens, min_tok));
+        if (w < 1)
+            w = 1;
+    }
+    w = std::min(w, ceil_div(total_tokens, p.block_tokens));
+    p.chunk = ceil_div(ceil_div(total_tokens, w), p.block_tokens) * p.block_tokens;
+    p.n_chunks = ceil_div(total_tokens, p.chunk);
+    p.n_slots = p.n_chunks + batch - 1;
+    p.xcd_remap = (p.n_chunks % 8 == 0) ? 1 : 0;
+    return p;
+}
+
+size_t partials_bytes(const Plan &p, int num_heads)
+{
+    const size_t rows = (size_t)p.n_slots * (size_t)num_heads;
+    return align_up(rows * kDV * sizeof(float)) + 2 * align_up(rows * sizeof(float));
+}
+
+Partials carve_partials(void *ws, const Plan &p, int num_heads)
+{
+    const size_t rows = (size_t)p.n_slots * (size_t)num_heads;
+    char *base = static_cast<char *>(ws);
+    Partials w;
+    w.o = reinterpret_cast<float *>(base);
+    base += align_up(rows * kDV * sizeof(float));
+    w.m = reinterpret_cast<float *>(base);
+    base += align_up(rows * sizeof(float));
+    w.l = reinterpret_cast<float *>(base);
+    return w;
+}
+
+namespace {
+
+bool heads_ok(int num_heads) { return num_heads > 0 && num_heads % 16 == 0 && num_heads <= 4096; }
+
+constexpr int kPhaseSplit = 1;
+constexpr int kPhaseCombine = 2;
+
+// Shared body of every entry point; `phases` selects the split kernel, the
+// combine, or both (in that order, on one stream).
+int run_decode(bool fp32, const void *query, const void *cache, const int *cu_seqlens,
+               void *out, void *workspace, size_t workspace_bytes, int batch,
+               int num_heads, int total_tokens, int num_splits, unsigned flags,
+               void *stream, int phases = kPhaseSplit | kPhaseCombine)
+{
+    const bool split = (phases & kPhaseSplit) != 0;
+    const bool combine = (phases & kPhaseCombine) != 0;
+    if (!workspace || (split && (!query || !cache)) || (combine && !out))
+        return MLA_STATUS_INVALID_VALUE;
+    if (!aligned16(workspace) || (split && (!aligned16(query) || !aligned16(cache))) ||
+        (combine && !aligned16(out)))
+        return MLA_STATUS_MISALIGNED;
+    const Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, current_cu_count());
+    if (workspace_bytes < partials_bytes(p, num_heads))
+        return MLA_STATUS_WORKSPACE_TOO_SMALL;
+
+    Problem pb;
+    pb.q = query;
+    pb.c = cache;
+    pb.cu_seqlens = cu_seqlens;
+    pb.out = out;
+    pb.batch = batch;
+    pb.num_heads = num_heads;
+    pb.total_tokens = total_tokens;
+    pb.scale_log2 = scale_log2();
+    const Partials w = carve_partials(workspace, p, num_heads);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    if (split) {
+        const hipError_t e = fp32 ? launch_splitkv_fp32(pb, p, w, s)
+                                  : launch_splitkv_fp16(pb, p, w, (flags & MLA_FLAG_SCALAR_TRANSPOSE) == 0, s);
+        if (e != hipSuccess)
+            return fail_hip(e);
+    }
+    if (combine) {
+        const hipError_t e = launch_combine(pb, p, w, fp32, s);
+        if (e != hipSuccess)
+            return fail_hip(e);
+    }
+    return MLA_STATUS_SUCCESS;
+}
+
+}  // namespace
+}  // namespace mla
+
+extern "C" {
+
+int mla_abi_version(void) { return MLA_ABI_VERSION; }
+
+const char *mla_status_string(int status)
+{
+    switch (status) {
+    case MLA_STATUS_SUCCESS: return "success";
+    case MLA_STATUS_INVALID_VALUE: return "invalid value (null pointer or unsupported size)";
+    case MLA_STATUS_MISALIGNED: return "pointer not 16-byte aligned";
+    case MLA_STATUS_WORKSPACE_TOO_SMALL: return "workspace too small";
+    case MLA_STATUS_HIP_ERROR: return "HIP error";
+    default: return "unknown status";
+    }
+}
+
+int mla_last_hip_error(void) { return mla::t_last_hip_error; }
+
+size_t mla_decode_split_workspace_size(int num_heads, int seq_length, int num_splits)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return 0;
+    const mla::Plan p = mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count());
+    return mla::partials_bytes(p, num_heads);
+}
+
+int mla_decode_split_fp16_ex(const void *query, const void *cache, void *out,
+                             void *workspace, size_t workspace_bytes,
+                             int num_heads, int seq_length, int num_splits,
+                             unsigned flags, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return MLA_STATUS_INVALID_VALUE;
+    return mla::run_decode(false, query, cache, nullptr, out, workspace, workspace_bytes, 1,
+                           num_heads, seq_length, num_splits, flags, stream);
+}
+
+int mla_decode_split_fp16(const void *query, const void *cache, void *out,
+                          void *workspace, size_t workspace_bytes,
+                          int num_heads, int seq_length, int num_splits, void *stream)
+{
+    return mla_decode_split_fp16_ex(query, cache, out, workspace, workspace_bytes, num_heads,
+                                    seq_length, num_splits, 0u, stream);
+}
+
+int mla_decode_split_fp16_partials(const void *query, const void *cache, void *workspace,
+                                   size_t workspace_bytes, int num_heads, int seq_length,
+                                   int num_splits, unsigned flags, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return MLA_STATUS_INVALID_VALUE;
+    return mla::run_decode(false, query, cache, nullptr, nullptr, workspace, workspace_bytes, 1,
+                           num_heads, seq_length, num_splits, flags, stream, mla::kPhaseSplit);
+}
+
+int mla_decode_split_fp16_combine(const void *workspace, size_t workspace_bytes, void *out,
+                                  int num_heads, int seq_length, int num_splits, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return MLA_STATUS_INVALID_VALUE;
+    return mla::run_decode(false, nullptr, nullptr, nullptr, out, const_cast<void *>(workspace),
+                           workspace_bytes, 1, num_heads, seq_length, num_splits, 0u, stream,
+                           mla::kPhaseCombine);
+}
+
+size_t mla_decode_fused_workspace_size(int num_heads, int seq_length, int num_splits)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return 0;
+    const mla::Plan p = mla::make_plan(true, num_heads, seq_length, 1, num_splits, mla::current_cu_count());
+    return mla::partials_bytes(p, num_heads);
+}
+
+int mla_decode_fused_fp32(const float *query, const float *cache, float *out,
+                          void *workspace, size_t workspace_bytes,
+                          int num_heads, int head_dim_c, int seq_length,
+                          int num_splits, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1 || head_dim_c != MLA_HEAD_DIM_K)
+        return MLA_STATUS_INVALID_VALUE;
+    return mla::run_decode(true, query, cache, nullptr, out, workspace, workspace_bytes, 1,
+                           num_heads, seq_length, num_splits, 0u, stream);
+}
+
+size_t mla_decode_split_batched_workspace_size(int batch, int num_heads, int total_tokens,
+                                               int num_splits)
+{
+    if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
+        return 0;
+    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, num_splits,
+                                       mla::current_cu_count());
+    return mla::partials_bytes(p, num_heads);
+}
+
+int mla_decode_split_batched_fp16(const void *query, const void *cache, const int *cu_seqlens,
+                                  void *out, void *workspace, size_t workspace_bytes,
+                                  int batch, int num_heads, int total_tokens, int num_splits,
+                                  void *stream)
+{
+    if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0 || !cu_seqlens)
+        return MLA_STATUS_INVALID_VALUE;
+    if (total_tokens == 0 && !cache)
+        cache = query;  // nothing is read from the cache
+    return mla::run_decode(false, query, cache, cu_seqlens, out, workspace, workspace_bytes, batch,
+                           num_heads, total_tokens, num_splits, 0u, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,62 @@
+// Device-side helpers for the gfx950 (CDNA4) MLA decode kernels: vector
+// types, MFMA wrappers, the LDS transpose read and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace mla {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef short shortx4 __attribute__((__vector_size__(4 * sizeof(short))));
+
+#define MLA_LDS __attribute__((address_space(3)))
+
+// D[16x16] += A[16x32] * B[32x16], fp16 in, fp32 accumulate.
+// Lane l supplies A[l % 16][8 * (l / 16) + j] and B[8 * (l / 16) + j][l % 16]
+// (j = 0..7) and holds D[4 * (l / 16) + i][l % 16] (i = 0..3).
+__device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// D[16x16] += A[16x4] * B[4x16] in fp32. Lane l supplies A[l % 16][l / 16]
+// and B[l / 16][l % 16]; D layout as above.
+__device__ __forceinline__ floatx4 mfma16x16x4f32(float a, float b, floatx4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane j points at the
+// 4 halves [row j / 4][4 * (j % 4) .. +3] of a 4 x 16 block; after the read,
+// lane i of the group holds column i of that block (rows 0..3).
+__device__ __forceinline__ half4 lds_read_tr16(const _Float16 *p)
+{
+    const MLA_LDS shortx4 *lp = (const MLA_LDS shortx4 *)(const MLA_LDS _Float16 *)p;
+    shortx4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<MLA_LDS shortx4 *>(lp));
+    return __builtin_bit_cast(half4, r);
+}
+
+// 2^x on the hardware exp unit (v_exp_f32); 2^-inf = 0.
+__device__ __forceinline__ float fast_exp2(float x)
+{
+    return __builtin_amdgcn_exp2f(x);
+}
+
+// max / sum over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float max_over_lane_groups(float v)
+{
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+__device__ __forceinline__ float sum_over_lane_groups(float v)
+{
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+}  // namespace mla

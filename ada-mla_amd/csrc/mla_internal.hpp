@@ -1,0 +1,63 @@
+// Host-side plan and launch interface shared by the kernel translation units
+// and the C ABI (mla_capi.hip). Not installed; callers use include/mla_mi355x.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+
+namespace mla {
+
+constexpr int kDK = 576;  // latent + rope width of Q* and C
+constexpr int kDV = 512;  // value width (C_N = C[:, :512])
+
+// Split-KV schedule. The packed token range [0, total_tokens) is cut into
+// n_chunks chunks of `chunk` tokens; workgroup (chunk w, head tile h) handles
+// heads [h * head_tile, +head_tile) over the tokens of chunk w. A chunk that
+// spans sequences b..b' emits one partial result per sequence; the partial of
+// (chunk w, sequence b) lives in slot w + b, so slots never collide and a
+// sequence's partials are the contiguous slots
+// [lo_b / chunk + b, (hi_b - 1) / chunk + b].
+struct Plan {
+    int head_tile;     // heads per workgroup
+    int n_head_tiles;  // num_heads / head_tile
+    int block_tokens;  // tokens per LDS block
+    int chunk;         // tokens per split (multiple of block_tokens)
+    int n_chunks;      // splits over the packed tokens
+    int n_slots;       // partial-result slots: n_chunks + batch - 1
+    int xcd_remap;     // 1: the head tiles of one chunk share an XCD
+};
+
+// Partial results of the split kernels (fp32): O unnormalised
+// [n_slots][num_heads][512], running max in log2 units and running sum
+// [n_slots][num_heads].
+struct Partials {
+    float *o;
+    float *m;
+    float *l;
+};
+
+struct Problem {
+    const void *q;          // [batch][num_heads][576]
+    const void *c;          // [total_tokens][576]
+    const int *cu_seqlens;  // [batch + 1] on device, or nullptr for one sequence
+    void *out;              // [batch][num_heads][512]
+    int batch;
+    int num_heads;
+    int total_tokens;
+    float scale_log2;       // softmax scale * log2(e)
+};
+
+Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
+               int num_splits, int cu_count);
+size_t partials_bytes(const Plan &p, int num_heads);
+Partials carve_partials(void *ws, const Plan &p, int num_heads);
+
+hipError_t launch_splitkv_fp16(const Problem &pb, const Plan &p,
+                               const Partials &w, bool tr_load, hipStream_t s);
+hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p,
+                               const Partials &w, hipStream_t s);
+hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
+                          bool out_fp32, hipStream_t s);
+
+}  // namespace mla

@@ -1,0 +1,136 @@
+/*
+ * mla_mi355x.h -- C ABI of the MI355X (gfx950) weight-absorbed MLA decode:
+ *
+ *     O*[h, :] = softmax_t( Q*[h, :] . C[t, :] / sqrt(192) ) . C[t, :512]
+ *
+ * with Q* [num_heads x 576], the latent cache C [N x 576] (first 512 columns
+ * are C_N, the last 64 the rope part) and O* [num_heads x 512].
+ *
+ * This is the drop-in boundary below the PyTorch extension: the reference's
+ * extension (csrc/mla_api.cpp) calls raw-pointer launchers declared in
+ * csrc/mla_decode.hpp; the entry points here are what it would bind instead.
+ *
+ * Conventions (all entry points):
+ *  - Plain device pointers, row-major and contiguous, 16-byte aligned.
+ *  - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
+ *    asynchronously; nothing synchronises, nothing allocates.
+ *  - The caller owns the workspace; query its size with the matching
+ *    *_workspace_size function (same arguments, same current device).
+ *    Calls that share one workspace must not overlap in time.
+ *  - `num_splits` <= 0 picks the split count from the sequence length and
+ *    the device's CU count; > 0 requests that many splits (clamped so every
+ *    split holds at least one LDS block).
+ *  - Return value: MLA_STATUS_SUCCESS (0) or one of the codes below; nothing
+ *    is enqueued when a code other than 0 or MLA_STATUS_HIP_ERROR is
+ *    returned. Thread-safe: no global mutable state besides a per-device
+ *    cache of the CU count and a thread-local last HIP error.
+ *  - num_heads must be a positive multiple of 16.
+ */
+#ifndef MLA_MI355X_H
+#define MLA_MI355X_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLA_HEAD_DIM_K 576 /* mla.py:33 HEAD_DIM_K = HEAD_DIM_C + HEAD_DIM_ROPE */
+#define MLA_HEAD_DIM_V 512 /* mla.py:31 HEAD_DIM_C */
+#define MLA_ABI_VERSION 1
+
+#define MLA_STATUS_SUCCESS 0
+#define MLA_STATUS_INVALID_VALUE 1       /* null pointer or unsupported size */
+#define MLA_STATUS_MISALIGNED 2          /* a pointer is not 16-byte aligned */
+#define MLA_STATUS_WORKSPACE_TOO_SMALL 3 /* workspace_bytes below the size query */
+#define MLA_STATUS_HIP_ERROR 4           /* a HIP launch failed: mla_last_hip_error() */
+
+/* Testing aid for mla_decode_split_fp16_ex: read the C_N^T operand of the
+ * second product with scalar LDS loads instead of the LDS transpose read. */
+#define MLA_FLAG_SCALAR_TRANSPOSE 1u
+
+int mla_abi_version(void);
+const char *mla_status_string(int status);
+/* hipError_t of the last failed HIP call on this thread (0 if none). */
+int mla_last_hip_error(void);
+
+/* Workspace for mla_decode_split_fp16 (fp32 split partials). Replaces the
+ * splits_max / splits_sum / splits_out buffers that mla_decode_split_
+ * allocates per call (csrc/mla_api.cpp:71-75). Returns 0 for invalid sizes. */
+size_t mla_decode_split_workspace_size(int num_heads, int seq_length,
+                                       int num_splits);
+
+/* fp16 split-KV decode: query [num_heads x 576] fp16, cache [seq_length x 576]
+ * fp16 -> out [num_heads x 512] fp16; fp32 accumulation, fp32 softmax state
+ * and fp32 partials. Replaces run_mla_decode_splitk<at::Half>
+ * (csrc/mla_decode.hpp:25-34; csrc/mla_decode_splitk_fwd_sm89.cu:26-47 ->
+ * run_mla_decode_splitk_fp16, csrc/mla_decode_splitk_fwd.cuh:941-985), which
+ * took three caller buffers, no stream, and required num_heads == 128 and
+ * seq_length % 64 == 0. */
+int mla_decode_split_fp16(const void *query, const void *cache, void *out,
+                          void *workspace, size_t workspace_bytes,
+                          int num_heads, int seq_length, int num_splits,
+                          void *stream);
+
+/* mla_decode_split_fp16 with flags (MLA_FLAG_*). */
+int mla_decode_split_fp16_ex(const void *query, const void *cache, void *out,
+                             void *workspace, size_t workspace_bytes,
+                             int num_heads, int seq_length, int num_splits,
+                             unsigned flags, void *stream);
+
+/* The two launches of mla_decode_split_fp16, one at a time: the split-KV
+ * kernel, which leaves fp32 partials in the workspace, then the LSE combine,
+ * which merges them into out. Called back to back on one stream with the
+ * same num_heads / seq_length / num_splits they equal mla_decode_split_fp16
+ * (the reference's launcher makes the same two launches,
+ * csrc/mla_decode_splitk_fwd.cuh:973-978); apart, they let a caller place
+ * other work or timing events between the phases. */
+int mla_decode_split_fp16_partials(const void *query, const void *cache,
+                                   void *workspace, size_t workspace_bytes,
+                                   int num_heads, int seq_length,
+                                   int num_splits, unsigned flags,
+                                   void *stream);
+int mla_decode_split_fp16_combine(const void *workspace,
+                                  size_t workspace_bytes, void *out,
+                                  int num_heads, int seq_length,
+                                  int num_splits, void *stream);
+
+/* Workspace for mla_decode_fused_fp32. */
+size_t mla_decode_fused_workspace_size(int num_heads, int seq_length,
+                                       int num_splits);
+
+/* fp32 decode: query [num_heads x head_dim_c] fp32, cache
+ * [seq_length x head_dim_c] fp32 -> out [num_heads x 512] fp32, fp32
+ * products. head_dim_c must be 576. Replaces run_mla_decode_fused
+ * (csrc/mla_decode.hpp:17-22; csrc/mla_decode_fused_fwd_sm89.cu:6-60), which
+ * needed num_heads % 16 == 0 and seq_length % 16 == 0 and no workspace. */
+int mla_decode_fused_fp32(const float *query, const float *cache, float *out,
+                          void *workspace, size_t workspace_bytes,
+                          int num_heads, int head_dim_c, int seq_length,
+                          int num_splits, void *stream);
+
+/* Workspace for mla_decode_split_batched_fp16. */
+size_t mla_decode_split_batched_workspace_size(int batch, int num_heads,
+                                               int total_tokens,
+                                               int num_splits);
+
+/* Batched variable-length fp16 decode (no reference counterpart: the
+ * reference handles one sequence per call, csrc/mla_api.cpp:67-69).
+ * query [batch x num_heads x 576] fp16; cache = the sequences' caches packed
+ * back to back [total_tokens x 576] fp16; cu_seqlens [batch + 1] int32 on the
+ * device with cu_seqlens[0] = 0, non-decreasing, cu_seqlens[batch] =
+ * total_tokens (sequence b owns rows cu_seqlens[b] .. cu_seqlens[b+1]-1);
+ * out [batch x num_heads x 512] fp16. Empty sequences give zero rows. The
+ * splits are cut over the packed tokens, so work is balanced whatever the
+ * length mix. Values of cu_seqlens outside [0, total_tokens] are clamped. */
+int mla_decode_split_batched_fp16(const void *query, const void *cache,
+                                  const int *cu_seqlens, void *out,
+                                  void *workspace, size_t workspace_bytes,
+                                  int batch, int num_heads, int total_tokens,
+                                  int num_splits, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLA_MI355X_H */

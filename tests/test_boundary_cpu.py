@@ -1,0 +1,139 @@
+"""CPU checks of the drop-in boundary: the C-ABI library loads and exports
+every function include/mla_mi355x.h declares, its argument validation
+returns the documented codes without launching anything, workspace sizes
+follow the split plan, and the torch extension rejects bad inputs. No
+compute call is made here (no GPU)."""
+import ctypes
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from ada_mla import capi
+
+
+def test_library_exports_every_declared_function():
+    lib = capi.load()
+    declared = capi.declared_functions()
+    assert len(declared) >= 10
+    for name in declared:
+        assert hasattr(lib, name), name
+    # and the dynamic symbol table agrees
+    syms = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH], capture_output=True,
+                          text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in syms.splitlines() if ln.strip()}
+    assert set(declared) <= exported
+
+
+def test_abi_version_and_status_strings():
+    lib = capi.load()
+    assert lib.mla_abi_version() == 1
+    assert lib.mla_status_string(0) == b"success"
+    assert b"workspace" in lib.mla_status_string(3)
+    assert lib.mla_status_string(99) == b"unknown status"
+
+
+def test_workspace_size_one_split():
+    lib = capi.load()
+    # one split: 128 heads x 512 fp32 partial O + 2 x 128 fp32 (256-byte aligned)
+    assert lib.mla_decode_split_workspace_size(128, 4096, 1) == 128 * 512 * 4 + 2 * 512
+    assert lib.mla_decode_fused_workspace_size(16, 100, 1) == 16 * 512 * 4 + 2 * 256
+
+
+def test_workspace_size_rejects_bad_sizes():
+    lib = capi.load()
+    assert lib.mla_decode_split_workspace_size(24, 4096, 0) == 0
+    assert lib.mla_decode_split_workspace_size(0, 4096, 0) == 0
+    assert lib.mla_decode_split_workspace_size(128, 0, 0) == 0
+    assert lib.mla_decode_split_batched_workspace_size(0, 128, 100, 0) == 0
+    assert lib.mla_decode_split_batched_workspace_size(4, 128, 0, 0) > 0  # all-empty batch is valid
+
+
+def test_workspace_grows_with_splits_and_batch():
+    lib = capi.load()
+    a = lib.mla_decode_split_workspace_size(128, 65536, 8)
+    b = lib.mla_decode_split_workspace_size(128, 65536, 64)
+    assert b == 8 * (a - 2 * 4096) + 2 * 32768
+    # batched: slots = splits + batch - 1
+    s = lib.mla_decode_split_batched_workspace_size(32, 128, 270000, 64)
+    assert s == (64 + 31) * 128 * 512 * 4 + 2 * ((64 + 31) * 128 * 4)
+
+
+def test_split_count_is_clamped_to_blocks():
+    lib = capi.load()
+    # 40 tokens cannot be cut into more than 2 blocks of 32 (128 heads -> 32-head tiles)
+    assert lib.mla_decode_split_workspace_size(128, 40, 1000) == lib.mla_decode_split_workspace_size(128, 40, 2)
+
+
+FAKE = 0x10000  # never dereferenced: every call below returns before any launch
+
+
+@pytest.mark.parametrize("args,code", [
+    ((None, FAKE, FAKE, FAKE, 1 << 30, 128, 64, 0, None), capi.STATUS_INVALID_VALUE),
+    ((FAKE, FAKE, FAKE, FAKE, 1 << 30, 24, 64, 0, None), capi.STATUS_INVALID_VALUE),
+    ((FAKE, FAKE, FAKE, FAKE, 1 << 30, 128, 0, 0, None), capi.STATUS_INVALID_VALUE),
+    ((FAKE + 2, FAKE, FAKE, FAKE, 1 << 30, 128, 64, 0, None), capi.STATUS_MISALIGNED),
+    ((FAKE, FAKE, FAKE, FAKE + 8, 1 << 30, 128, 64, 0, None), capi.STATUS_MISALIGNED),
+    ((FAKE, FAKE, FAKE, FAKE, 16, 128, 64, 0, None), capi.STATUS_WORKSPACE_TOO_SMALL),
+])
+def test_split_fp16_argument_errors(args, code):
+    assert capi.load().mla_decode_split_fp16(*args) == code
+
+
+def test_fused_fp32_rejects_head_dim():
+    lib = capi.load()
+    assert lib.mla_decode_fused_fp32(FAKE, FAKE, FAKE, FAKE, 1 << 30, 128, 512, 64, 0, None) == \
+        capi.STATUS_INVALID_VALUE
+    assert lib.mla_decode_fused_fp32(FAKE, FAKE, FAKE, FAKE, 16, 128, 576, 64, 0, None) == \
+        capi.STATUS_WORKSPACE_TOO_SMALL
+
+
+def test_batched_argument_errors():
+    lib = capi.load()
+    f = lib.mla_decode_split_batched_fp16
+    assert f(FAKE, FAKE, None, FAKE, FAKE, 1 << 30, 4, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30, 0, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 16, 4, 128, 100, 0, None) == capi.STATUS_WORKSPACE_TOO_SMALL
+
+
+# --------------------------------------------------------- torch extension
+
+def _ext():
+    import ada_mla
+    return ada_mla
+
+
+def test_extension_surface():
+    m = _ext()
+    assert m.HEAD_DIM_K == 576 and m.HEAD_DIM_C == 512 and m.HEAD_DIM_ROPE == 64
+    for fn in ("mla_decode_split", "mla_decode_fused", "mla_decode_split_batched"):
+        assert callable(getattr(m, fn))
+
+
+@pytest.mark.parametrize("q,c,msg", [
+    (torch.zeros(128, 576, dtype=torch.float16), torch.zeros(64, 576, dtype=torch.float32), "same dtype"),
+    (torch.zeros(128, 576, dtype=torch.bfloat16), torch.zeros(64, 576, dtype=torch.bfloat16), "float16 or float32"),
+    (torch.zeros(128, 576, dtype=torch.float16), torch.zeros(64, 577, dtype=torch.float16), "cache must be"),
+    (torch.zeros(128, 576, dtype=torch.float16), torch.zeros(0, 576, dtype=torch.float16), "at least one token"),
+    (torch.zeros(128, 512, dtype=torch.float16), torch.zeros(64, 576, dtype=torch.float16), "query must be"),
+    (torch.zeros(24, 576, dtype=torch.float16), torch.zeros(64, 576, dtype=torch.float16), "multiple of 16"),
+    (torch.zeros(128, 576, dtype=torch.float16), torch.zeros(64, 576, dtype=torch.float16), "GPU tensors"),
+])
+def test_extension_rejects_bad_inputs(q, c, msg):
+    m = _ext()
+    for fn in (m.mla_decode_split, m.mla_decode_fused):
+        with pytest.raises(RuntimeError, match=msg):
+            fn(q, c)
+
+
+def test_batched_extension_rejects_bad_inputs():
+    m = _ext()
+    q = torch.zeros(2, 128, 576, dtype=torch.float16)
+    c = torch.zeros(10, 576, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="batch \\+ 1"):
+        m.mla_decode_split_batched(q, c, torch.zeros(2, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="int32"):
+        m.mla_decode_split_batched(q, c, torch.zeros(3, dtype=torch.int64))
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        m.mla_decode_split_batched(q, c, torch.zeros(3, dtype=torch.int32))
