@@ -69,11 +69,11 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
         p.head_tile = 16;
         p.block_tokens = 16;
     } else {
-        p.head_tile = (num_heads % 32 == 0) ? 32 : 16;
-        p.block_tokens = (p.head_tile == 32) ? 32 : 64;
+        p.head_tile = (num_heads % 64 == 0) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
+        p.block_tokens = 32;
     }
     p.n_head_tiles = num_heads / p.head_tile;
-    const int wgs_per_cu = (!fp32 && p.head_tile == 32) ? 2 : 1;
+    const int wgs_per_cu = 1;
     if (total_tokens <= 0) {
         p.chunk = p.block_tokens;
         p.n_chunks = 0;
@@ -189,6 +189,13 @@ const char *mla_status_string(int status)
 }
 
 int mla_last_hip_error(void) { return mla::t_last_hip_error; }
+
+int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return 0;
+    return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count()).n_chunks;
+}
 
 size_t mla_decode_split_workspace_size(int num_heads, int seq_length, int num_splits)
 {

@@ -1,27 +1,36 @@
 // fp16 split-KV MLA decode for gfx950:
-//   O*_partial = sum_t exp2(s_t - m) C_N[t],  s_t = log2(e) * scale * (Q* . C[t])
+//   O*_partial = sum_t 2^(s_t - m) C_N[t],  s_t = log2(e) * scale * (Q* . C[t])
 // for one (chunk of tokens, tile of heads) per workgroup, written as fp32
 // partials (O unnormalised, running max m, running sum l) that
 // mla_combine.hip merges.
 //
 // Replaces mla_decode_splitk_mma_fp16 (reference
 // csrc/mla_decode_splitk_fwd.cuh:559-892), with a different design:
-//  * 256 threads = 4 wave64s. Each C block (kBT tokens x 576) is staged once
-//    in LDS and read by both products.
-//  * Q* C^T is computed as S^T = C Q*^T on 16x16x32 MFMAs: wave w owns a
-//    16-token x 16-head tile over the full K = 576, with its Q* fragment
-//    resident in VGPRs for the whole chunk (no K slicing, no cross-wave sum
-//    of logits).
+//  * 512 threads = 8 wave64s, one workgroup per CU, in two roles with one
+//    wave of each role on every SIMD, so that one role's LDS and softmax
+//    latencies hide behind the other role's MFMAs:
+//      - S waves (HT/16 of them) compute the logits and the online softmax
+//        of block t+1: S^T = C Q*^T on 16x16x32 MFMAs, each wave owning 16
+//        heads x 32 tokens over the full K = 576 (eight independent
+//        accumulation chains) with its Q* fragment resident in registers,
+//        so no wave needs another wave's logits;
+//      - O waves (4) accumulate block t: O^T = C_N^T P^T, each owning 128
+//        output columns for all heads of the tile, with the C_N^T operand
+//        read from the ring slot by the LDS transpose read
+//        (ds_read_b64_tr_b16); they also feed the ring.
+//    P (fp16) and the rescale factors pass from S to O waves through a
+//    double-buffered LDS area; one workgroup barrier per block.
+//  * C streams through a 4-slot LDS ring of 32-token blocks filled by
+//    direct global->LDS loads (global_load_lds_dwordx4), two blocks ahead of
+//    the S waves; each block is read from LDS by both products.
 //  * Online softmax in fp32 (log2 domain), running max started at -inf; the
-//    per-head block max crosses the 4 lane groups with shuffles and the token
-//    tiles through a 128-byte LDS exchange.
-//  * P C_N is computed as O^T = C_N^T P^T: wave w owns 128 output columns for
-//    all heads of the tile, so the online-softmax rescale is one scalar per
-//    lane; the C_N^T operand comes straight from the staged block with the
-//    LDS transpose read (ds_read_b64_tr_b16).
-//  * The next block is prefetched into VGPRs one iteration ahead and written
-//    to the other LDS slot between the two barriers of each iteration, so a
-//    slot is never overwritten while any wave still reads it.
+//    O rescale is skipped when no head's max moved (exact: the factor is 1).
+//  * Rows of a ring slot are XOR-swizzled in 16-byte chunks so that both the
+//    row-wise reads of the first product and the transpose reads of the
+//    second hit distinct LDS banks.
+//  * Barriers are plain s_barrier after an LDS counter wait: the
+//    global->LDS loads are tracked with explicit vmcnt waits by the waves
+//    that issue them, so a barrier never drains the loads in flight.
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
 
@@ -30,21 +39,79 @@ namespace {
 
 template <int HT>
 struct F16Tile {
-    static constexpr int kNHS = HT / 16;                    // 16-head sub-tiles
-    static constexpr int kNTT = 4 / kNHS;                   // 16-token tiles per block
-    static constexpr int kBT = 16 * kNTT;                   // tokens per block
-    static constexpr int kRow = kDK + 8;                    // LDS row stride (halves)
-    static constexpr int kRowChunks = kDK / 8;              // 16-byte chunks per row
-    static constexpr int kStage = kBT * kRowChunks / 256;   // chunks per thread
-    static constexpr int kPRow = kBT + 8;                   // P row stride (halves)
-    static constexpr int kK2 = kBT / 32;                    // P C_N k-steps per block
-    static_assert(kBT * kRowChunks % 256 == 0, "stage split");
-    static_assert(kBT % 32 == 0, "P C_N k-step");
+    static constexpr int kWaves = 8;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kBT = 32;                      // tokens per block
+    static constexpr int kRing = 4;                     // LDS ring slots
+    static constexpr int kSWaves = HT / 16;             // S waves (16 heads each)
+    static constexpr int kOWave0 = 4;                   // O waves are 4..7
+    static constexpr int kNHS = HT / 16;                // 16-head sub-tiles per tile
+    static constexpr int kChains = 4;                   // accumulation chains per S^T tile
+    static constexpr int kSlot = kBT * kDK;             // halves per slot (36 KB)
+    static constexpr int kUnits = kSlot * 2 / 1024;     // 1 KB load units per slot
+    static constexpr int kLoadsPerWave = kUnits / 4;    // per O wave per block
+    static constexpr int kPRow = kBT + 8;               // P row stride (halves)
+    // Q* of the head tile is staged through the top ring slots at the start
+    // of each piece (HT rows of 1152 bytes, swizzled like C rows).
+    static constexpr int kQUnits = HT * kDK * 2 / 1024;
+    static constexpr int kQLoadsPerWave = (kQUnits + 3) / 4;
+    static constexpr int kQSlots = (HT * kDK + kSlot - 1) / kSlot;
+    static constexpr int kPreBlocks = kRing - kQSlots;  // blocks issued with Q*
+    static_assert(kUnits % 4 == 0, "units per wave");
+    static_assert(kSWaves <= kOWave0, "S waves");
+    static_assert(kQSlots >= 1 && kQSlots <= 2, "Q slots");
 };
 
+// XOR swizzle of the 16-byte chunk index within a 1152-byte row. Bits of the
+// row (mod 16) are permuted so that 16 consecutive rows at one chunk hit 16
+// distinct chunk positions (S^T operand reads), and the 32-byte chunk pairs
+// read by the transpose loads of rows {r..r+3, r+8..r+11} land on 8 distinct
+// pairs. Chunks 64..71 (the rope columns, never read transposed) use the low
+// 3 bits only so they stay inside their 8-chunk group.
+__device__ __forceinline__ int row_swizzle(int row)
+{
+    return ((row >> 2) & 1) | ((row & 3) << 1) | (row & 8);
+}
+
+__device__ __forceinline__ int phys_chunk(int c, int swz)
+{
+    return c < 64 ? (c ^ swz) : (c ^ (swz & 7));
+}
+
+// s_waitcnt vmcnt(n) leaving the other counters unconstrained.
+#define MLA_WAIT_VMCNT(n) \
+    __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (7 << 4) | (0xF << 8))
+
+// Workgroup barrier that waits only for this wave's LDS operations; the
+// memory clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// 16 bytes per lane from base + off (bytes) into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4; lds must be wave-uniform). Issued as inline asm
+// so that the compiler does not model it: it would otherwise wait for every
+// such load before each LDS read. The kernel orders these loads itself with
+// MLA_WAIT_VMCNT; the compiler's own vmcnt waits stay correct because
+// vector-memory loads retire in order, so loads it does not count only make
+// its waits more conservative.
+__device__ __forceinline__ void global_to_lds16(const _Float16 *base, int off, const void *lds)
+{
+    const unsigned l = __builtin_amdgcn_readfirstlane(
+        (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+    unsigned saved_m0;
+    // m0 carries the LDS address; its previous value is restored so the asm
+    // leaves the (compiler-reserved) register unchanged.
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %3\n\t"
+                 "global_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved_m0) : "v"(off), "s"(base), "s"(l) : "memory");
+}
+
 template <int HT, bool kTr>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256),
-                          amdgpu_waves_per_eu(HT == 32 ? 2 : 1, HT == 32 ? 2 : 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                          const _Float16 *__restrict__ c,
                          const int *__restrict__ cu_seqlens,
@@ -55,13 +122,13 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                          int n_head_tiles, int xcd_remap, float scale_log2)
 {
     using T = F16Tile<HT>;
-    __shared__ __attribute__((aligned(16))) _Float16 s_c[2 * T::kBT * T::kRow];
-    __shared__ __attribute__((aligned(16))) _Float16 s_p[HT * T::kPRow];
-    __shared__ float s_red[T::kNTT * HT];
+    __shared__ __attribute__((aligned(1024))) _Float16 s_ring[T::kRing * T::kSlot];
+    __shared__ __attribute__((aligned(16))) _Float16 s_p[2][HT * T::kPRow];
+    __shared__ float s_alpha[2][HT];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
 
@@ -86,8 +153,10 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
     if (lo >= hi)
         return;
 
-    const int hs1 = wave % T::kNHS;  // head sub-tile of this wave's logits
-    const int tt = wave / T::kNHS;   // token tile of this wave's logits
+    const bool s_wave = wave < T::kSWaves;   // logits + softmax of 16 heads
+    const bool o_wave = wave >= T::kOWave0;  // 128 output columns + ring loads
+    const int hg = s_wave ? wave : 0;        // S wave: its 16-head group
+    const int ow = wave - T::kOWave0;        // O wave: its column quarter
     const int head0 = ht * HT;
 
     // First sequence containing token lo (largest b with cu[b] <= lo).
@@ -102,6 +171,20 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
         b = l;
     }
 
+    // Per-lane chunk offsets of the S^T operand reads (rows 16*tt + l16,
+    // logical chunk 4*kk + g). For kk < 16 the swizzle permutes kk within
+    // aligned groups of 4 and g within 0..3, so four offsets plus immediates
+    // cover them; the rope chunks 64..71 have two more.
+    const int swz_a = row_swizzle(l16);
+    int a_off[6];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        a_off[j] = 8 * (4 * (j ^ (swz_a >> 2)) + ((g ^ swz_a) & 3));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        a_off[4 + j] = 8 * (64 + ((4 * j + g) ^ (swz_a & 7)));
+    auto a_chunk = [&](int kk) { return kk < 16 ? a_off[kk & 3] + 128 * (kk >> 2) : a_off[kk - 12]; };
+
     for (; b < nseq; ++b) {
         int seq_lo = 0, seq_hi = total_tokens;
         if (cu_seqlens) {
@@ -114,186 +197,222 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
         const int p_hi = min(seq_hi, hi);
         if (p_lo >= p_hi)
             continue;
-        const int slot = split + b;
+        const int slot_out = split + b;
         const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
 
-        __syncthreads();  // LDS is reused from the previous piece
+        lds_barrier();  // the ring and the P / alpha buffers are reused from the previous piece
 
-        // Q* fragment (B operand of S^T = C Q*^T): lane holds head
-        // head0 + 16*hs1 + l16, dims 32*kk + 8*g .. +7.
-        half8 qf[kDK / 32];
-        {
-            const _Float16 *qrow = q + ((size_t)b * num_heads + head0 + 16 * hs1 + l16) * kDK + 8 * g;
+        // Global -> LDS load of block `blk` into ring slot blk % kRing by the
+        // O waves. Load unit u (1 KB) = chunk positions [64u, 64u + 64) of
+        // the slot; lane l fetches the logical chunk stored at position
+        // 64u + l. Rows past the end of the piece re-read its last token
+        // (finite data, masked later); a block past the last one re-reads
+        // only that token.
+        auto issue_block = [&](int blk) {
+            const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
+            const int lim = p_hi - 1 - t0;
+            const _Float16 *base = c + (size_t)t0 * kDK;
+            _Float16 *slot = s_ring + (blk % T::kRing) * T::kSlot;
 #pragma unroll
-            for (int kk = 0; kk < kDK / 32; ++kk)
-                qf[kk] = *(const half8 *)(qrow + 32 * kk);
+            for (int k = 0; k < T::kLoadsPerWave; ++k) {
+                const int u = ow + 4 * k;
+                const int pos = 64 * u + lane;
+                const int row = pos / 72;
+                const int pc = pos - 72 * row;
+                const int lc = phys_chunk(pc, row_swizzle(row));
+                global_to_lds16(base, (min(row, lim) * kDK + lc * 8) * 2, slot + u * 512);
+            }
+        };
+
+        // Prologue: Q* rows of this head tile go to the top kQSlots ring
+        // slots (their blocks are not needed yet), blocks 0.. to the others;
+        // blocks 0..2 are always issued (past the last block as re-reads of
+        // the last token), so every wait count is a constant.
+        if (o_wave) {
+            const _Float16 *qbase = q + ((size_t)b * num_heads + head0) * kDK;
+            _Float16 *qslot = s_ring + T::kPreBlocks * T::kSlot;
+#pragma unroll
+            for (int k = 0; k < T::kQLoadsPerWave; ++k) {
+                const int u = min(ow + 4 * k, T::kQUnits - 1);
+                const int pos = 64 * u + lane;
+                const int row = pos / 72;
+                const int pc = pos - 72 * row;
+                global_to_lds16(qbase, (row * kDK + 8 * phys_chunk(pc, row_swizzle(row))) * 2,
+                                qslot + u * 512);
+            }
+#pragma unroll
+            for (int blk = 0; blk < T::kPreBlocks; ++blk)
+                issue_block(blk);
+            MLA_WAIT_VMCNT(T::kPreBlocks * T::kLoadsPerWave);  // Q* has landed
         }
+        lds_barrier();
 
-        half8 stage[T::kStage];
-        auto load_stage = [&](int t0) {
-#pragma unroll
-            for (int s = 0; s < T::kStage; ++s) {
-                const int ci = tid + 256 * s;
-                const int tok = ci / T::kRowChunks;
-                const int col = ci - tok * T::kRowChunks;
-                const int gt = t0 + tok;
-                if (gt < p_hi)
-                    stage[s] = *(const half8 *)(c + (size_t)gt * kDK + col * 8);
-                else
-                    stage[s] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-            }
-        };
-        auto store_stage = [&](int which) {
-            _Float16 *dst = s_c + which * T::kBT * T::kRow;
-#pragma unroll
-            for (int s = 0; s < T::kStage; ++s) {
-                const int ci = tid + 256 * s;
-                const int tok = ci / T::kRowChunks;
-                const int col = ci - tok * T::kRowChunks;
-                *(half8 *)(dst + tok * T::kRow + col * 8) = stage[s];
-            }
-        };
-
-        load_stage(p_lo);
-        store_stage(0);
-        if (nblk > 1)
-            load_stage(p_lo + T::kBT);
-
-        float m_run[T::kNHS];
-#pragma unroll
-        for (int hs = 0; hs < T::kNHS; ++hs)
-            m_run[hs] = -INFINITY;
-        float l_run = 0.f;
-        floatx4 o[T::kNHS][8];
-#pragma unroll
-        for (int hs = 0; hs < T::kNHS; ++hs)
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt)
-                o[hs][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-        __syncthreads();
-
-        for (int blk = 0; blk < nblk; ++blk) {
-            const int cur = blk & 1;
-            const int t0 = p_lo + blk * T::kBT;
-            const _Float16 *cs = s_c + cur * T::kBT * T::kRow;
-
-            // ---- S^T tile: tokens t0 + 16*tt + (0..15), heads 16*hs1 + (0..15)
-            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        // Each role runs its own copy of the step loop (t = -1 .. nblk-1,
+        // S waves on block t+1, O waves on block t) with the same sequence of
+        // barriers, so that the registers of one role (Q* fragments, logit
+        // accumulators) and of the other (O accumulators) can share space.
+        if (s_wave) {
+            // Q* fragment (B operand of S^T = C Q*^T): lane holds head
+            // 16*hg + l16 of the tile, dims 32*kk + 8*g .. +7.
+            half8 qf[kDK / 32];
             {
-                const _Float16 *arow = cs + (16 * tt + l16) * T::kRow + 8 * g;
+                const _Float16 *qs = s_ring + T::kPreBlocks * T::kSlot + (16 * hg + l16) * kDK;
 #pragma unroll
                 for (int kk = 0; kk < kDK / 32; ++kk)
-                    acc = mfma16x16x32(*(const half8 *)(arow + 32 * kk), qf[kk], acc);
+                    qf[kk] = *(const half8 *)(qs + a_chunk(kk));
             }
+            lds_barrier();  // Q* slots are free again
+            lds_barrier();  // block 0 has landed
 
-            // ---- block max per head (log2 units), masked tail tokens = -inf
-            float sv[4];
-            float mx = -INFINITY;
+            float m_run = -INFINITY, l_run = 0.f;  // head 16*hg + l16
+            for (int t = -1; t < nblk; ++t) {
+                if (t + 1 < nblk) {
+                    const int blk = t + 1;
+                    const int t0 = p_lo + blk * T::kBT;
+                    const _Float16 *cs = s_ring + (blk % T::kRing) * T::kSlot;
+                    // ---- S^T tiles: tokens t0 + 16*tt + (0..15), heads 16*hg + (0..15)
+                    floatx4 acc[2][T::kChains];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int tok = t0 + 16 * tt + 4 * g + i;
-                sv[i] = tok < p_hi ? acc[i] * scale_log2 : -INFINITY;
-                mx = fmaxf(mx, sv[i]);
-            }
-            mx = max_over_lane_groups(mx);
-            if (g == 0)
-                s_red[tt * HT + 16 * hs1 + l16] = mx;
-            __syncthreads();
-
-            // ---- new running max for every head sub-tile this wave touches
-            float alpha[T::kNHS];
+                    for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int hs = 0; hs < T::kNHS; ++hs) {
-                float mb = s_red[16 * hs + l16];
+                        for (int j = 0; j < T::kChains; ++j)
+                            acc[tt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int t2 = 1; t2 < T::kNTT; ++t2)
-                    mb = fmaxf(mb, s_red[t2 * HT + 16 * hs + l16]);
-                const float mn = fmaxf(m_run[hs], mb);
-                alpha[hs] = fast_exp2(m_run[hs] - mn);
-                m_run[hs] = mn;
-            }
-            {
-                float mcur = m_run[0];
-                float acur = alpha[0];
+                    for (int kk = 0; kk < kDK / 32; ++kk)
 #pragma unroll
-                for (int hs = 1; hs < T::kNHS; ++hs)
-                    if (hs == hs1) { mcur = m_run[hs]; acur = alpha[hs]; }
-                half4 ph;
-                float psum = 0.f;
+                        for (int tt = 0; tt < 2; ++tt)
+                            acc[tt][kk % T::kChains] = mfma16x16x32(
+                                *(const half8 *)(cs + (16 * tt + l16) * kDK + a_chunk(kk)), qf[kk],
+                                acc[tt][kk % T::kChains]);
+                    // ---- online softmax over the block for this wave's heads
+                    float sv[2][4];
+                    float mx = -INFINITY;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = fast_exp2(sv[i] - mcur);
-                    psum += p;
-                    ph[i] = (_Float16)p;
+                    for (int tt = 0; tt < 2; ++tt) {
+                        const floatx4 st = (acc[tt][0] + acc[tt][1]) + (acc[tt][2] + acc[tt][3]);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int tok = t0 + 16 * tt + 4 * g + i;
+                            sv[tt][i] = tok < p_hi ? st[i] * scale_log2 : -INFINITY;
+                            mx = fmaxf(mx, sv[tt][i]);
+                        }
+                    }
+                    mx = max_over_lane_groups(mx);
+                    const float mn = fmaxf(m_run, mx);
+                    const float alpha = fast_exp2(m_run - mn);
+                    m_run = mn;
+                    float psum = 0.f;
+                    _Float16 *prow = s_p[blk & 1] + (16 * hg + l16) * T::kPRow + 4 * g;
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+                        half4 ph;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float p = fast_exp2(sv[tt][i] - mn);
+                            psum += p;
+                            ph[i] = (_Float16)p;
+                        }
+                        *(half4 *)(prow + 16 * tt) = ph;
+                    }
+                    l_run = l_run * alpha + psum;
+                    if (g == 0)
+                        s_alpha[blk & 1][16 * hg + l16] = alpha;
                 }
-                l_run = l_run * acur + psum;
-                *(half4 *)(s_p + (16 * hs1 + l16) * T::kPRow + 16 * tt + 4 * g) = ph;
+                lds_barrier();
             }
+            // ---- epilogue: m and l of this wave's heads
+            const float ls = sum_over_lane_groups(l_run);
+            if (g == 0) {
+                m_part[(size_t)slot_out * num_heads + head0 + 16 * hg + l16] = m_run;
+                l_part[(size_t)slot_out * num_heads + head0 + 16 * hg + l16] = ls;
+            }
+        } else if (o_wave) {
+            lds_barrier();  // Q* slots are free again
+#pragma unroll
+            for (int blk = T::kPreBlocks; blk < T::kRing - 1; ++blk)
+                issue_block(blk);
+            // block 0 has landed; blocks 1 and 2 may stay in flight
+            MLA_WAIT_VMCNT(2 * T::kLoadsPerWave);
+            lds_barrier();
 
-            if (blk + 1 < nblk)
-                store_stage(cur ^ 1);
-            if (blk + 2 < nblk)
-                load_stage(t0 + 2 * T::kBT);
-            __syncthreads();
-
-            // ---- O^T[dims 128*wave .. +128][heads] += C_N^T P^T
+            floatx4 o[T::kNHS][8];
 #pragma unroll
             for (int hs = 0; hs < T::kNHS; ++hs)
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt)
-                    o[hs][dt] *= alpha[hs];
+                    o[hs][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+            for (int t = -1; t < nblk; ++t) {
+                if (t >= 0 && t + T::kRing - 1 < nblk)
+                    issue_block(t + T::kRing - 1);  // into the slot block t-1 left
+                if (t >= 0) {
+                    const int blk = t;
+                    const _Float16 *cs = s_ring + (blk % T::kRing) * T::kSlot;
+                    // ---- rescale, skipped when no head's max moved
+                    float alpha[T::kNHS];
+                    bool moved = false;
 #pragma unroll
-            for (int ks = 0; ks < T::kK2; ++ks) {
-                half8 pb[T::kNHS];
-#pragma unroll
-                for (int hs = 0; hs < T::kNHS; ++hs)
-                    pb[hs] = *(const half8 *)(s_p + (16 * hs + l16) * T::kPRow + 32 * ks + 8 * g);
-#pragma unroll
-                for (int dt = 0; dt < 8; ++dt) {
-                    const int d0 = 128 * wave + 16 * dt;
-                    half8 a;
-                    if constexpr (kTr) {
-                        const _Float16 *p = cs + (32 * ks + 8 * g + (l16 >> 2)) * T::kRow + d0 + 4 * (l16 & 3);
-                        const half4 lo4 = lds_read_tr16(p);
-                        const half4 hi4 = lds_read_tr16(p + 4 * T::kRow);
-                        a = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-                    } else {
-                        const _Float16 *p = cs + (32 * ks + 8 * g) * T::kRow + d0 + l16;
-#pragma unroll
-                        for (int j = 0; j < 8; ++j)
-                            a[j] = p[j * T::kRow];
+                    for (int hs = 0; hs < T::kNHS; ++hs) {
+                        alpha[hs] = s_alpha[blk & 1][16 * hs + l16];
+                        moved |= alpha[hs] != 1.0f;
                     }
+                    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+#pragma unroll
+                        for (int hs = 0; hs < T::kNHS; ++hs)
+#pragma unroll
+                            for (int dt = 0; dt < 8; ++dt)
+                                o[hs][dt] *= alpha[hs];
+                    }
+                    // ---- O^T[dims 128*ow .. +128][heads] += C_N^T P^T
+                    half8 pb[T::kNHS];
 #pragma unroll
                     for (int hs = 0; hs < T::kNHS; ++hs)
-                        o[hs][dt] = mfma16x16x32(a, pb[hs], o[hs][dt]);
+                        pb[hs] = *(const half8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) {
+                        half8 a;
+                        if constexpr (kTr) {
+                            // lane (g, j): rows 8g + j/4 (+4), dims 128*ow + 16*dt + 4*(j%4) .. +3
+                            const int r0 = 8 * g + (l16 >> 2);
+                            const int cl = 16 * ow + 2 * dt + ((l16 & 3) >> 1);
+                            const int sub = 4 * (l16 & 1);
+                            const _Float16 *p0 = cs + r0 * kDK + 8 * phys_chunk(cl, row_swizzle(r0)) + sub;
+                            const _Float16 *p1 = cs + (r0 + 4) * kDK + 8 * phys_chunk(cl, row_swizzle(r0 + 4)) + sub;
+                            const half4 lo4 = lds_read_tr16(p0);
+                            const half4 hi4 = lds_read_tr16(p1);
+                            a = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                        } else {
+                            const int col = 128 * ow + 16 * dt + l16;
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                const int r = 8 * g + j;
+                                a[j] = cs[r * kDK + 8 * phys_chunk(col >> 3, row_swizzle(r)) + (col & 7)];
+                            }
+                        }
+#pragma unroll
+                        for (int hs = 0; hs < T::kNHS; ++hs)
+                            o[hs][dt] = mfma16x16x32(a, pb[hs], o[hs][dt]);
+                    }
                 }
+                // ---- block t+2 (the S waves' next-but-one) must have landed
+                // before the barrier; block t+3 may stay in flight
+                if (t >= 0 && t + T::kRing - 1 < nblk) MLA_WAIT_VMCNT(T::kLoadsPerWave);
+                else MLA_WAIT_VMCNT(0);
+                lds_barrier();
             }
-        }
-
-        // ---- epilogue: partial (O, m, l) of this piece into its slot
-        const float lsum = sum_over_lane_groups(l_run);
-        if (g == 0)
-            s_red[tt * HT + 16 * hs1 + l16] = lsum;  // s_red reads all ended before the last barrier
-        __syncthreads();
-        if (tid < HT) {
-            float L = 0.f;
+            // ---- epilogue: the unnormalised O of this piece
+            float *obase = o_part + ((size_t)slot_out * num_heads + head0 + l16) * kDV + 128 * ow + 4 * g;
 #pragma unroll
-            for (int t2 = 0; t2 < T::kNTT; ++t2)
-                L += s_red[t2 * HT + tid];
-            float mv = m_run[0];
+            for (int hs = 0; hs < T::kNHS; ++hs)
 #pragma unroll
-            for (int hs = 1; hs < T::kNHS; ++hs)
-                if ((tid >> 4) == hs) mv = m_run[hs];
-            m_part[(size_t)slot * num_heads + head0 + tid] = mv;
-            l_part[(size_t)slot * num_heads + head0 + tid] = L;
-        }
-#pragma unroll
-        for (int hs = 0; hs < T::kNHS; ++hs) {
-            float *orow = o_part + ((size_t)slot * num_heads + head0 + 16 * hs + l16) * kDV + 128 * wave + 4 * g;
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt)
-                *(floatx4 *)(orow + 16 * dt) = o[hs][dt];
+                for (int dt = 0; dt < 8; ++dt)
+                    *(floatx4 *)(obase + 16 * hs * kDV + 16 * dt) = o[hs][dt];
+        } else {
+            // waves with no role at this head-tile size keep the barrier count
+            lds_barrier();
+            lds_barrier();
+            for (int t = -1; t < nblk; ++t)
+                lds_barrier();
         }
     }
 }
@@ -301,7 +420,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
 template <int HT, bool kTr>
 hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStream_t s)
 {
-    const dim3 grid(p.n_chunks * p.n_head_tiles), block(256);
+    const dim3 grid(p.n_chunks * p.n_head_tiles), block(F16Tile<HT>::kThreads);
     hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr>), grid, block, 0, s,
                        (const _Float16 *)pb.q, (const _Float16 *)pb.c, pb.cu_seqlens,
                        w.o, w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
@@ -316,9 +435,11 @@ hipError_t launch_splitkv_fp16(const Problem &pb, const Plan &p, const Partials 
 {
     if (p.n_chunks == 0)
         return hipSuccess;
-    if (p.head_tile == 32)
-        return tr_load ? launch_ht<32, true>(pb, p, w, s) : launch_ht<32, false>(pb, p, w, s);
-    return tr_load ? launch_ht<16, true>(pb, p, w, s) : launch_ht<16, false>(pb, p, w, s);
+    switch (p.head_tile) {
+    case 64: return tr_load ? launch_ht<64, true>(pb, p, w, s) : launch_ht<64, false>(pb, p, w, s);
+    case 32: return tr_load ? launch_ht<32, true>(pb, p, w, s) : launch_ht<32, false>(pb, p, w, s);
+    default: return tr_load ? launch_ht<16, true>(pb, p, w, s) : launch_ht<16, false>(pb, p, w, s);
+    }
 }
 
 }  // namespace mla

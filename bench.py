@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""MLA decode benchmark on one MI355X.
+
+Metric: microseconds per MLA decode call + achieved HBM TB/s,
+n_h = 128, N = 4096, fp16 -- the reference's `-k fused` fp16 path
+(mla_decode_split, csrc/mla_api.cpp:86-113), here through the C ABI of
+libmla_mi355x.so.
+
+A step is one decode call (split-KV kernel + LSE combine) over one
+synthetic (Q*, C) pair. Inputs are resident in HBM before timing starts;
+each step uses the next pair of a pool of distinct buffers totalling
+--flush-mb (default 1024 MB > the 256 MB MALL + 32 MB of L2), so no step
+finds its C in a cache. Timing is HIP events on the launch stream: one pair
+around all K steps (value, us/call) and one pair around each split-kernel
+launch (roofline.achieved for the dominant kernel).
+
+Prints ONE JSON line. --workload picks another configuration (n65536, nh16,
+batched, fp32) for measurement runs; the default is the headline one.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "ada-mla_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "µs per MLA decode call + achieved HBM TB/s, n_h=128 N=4096 fp16"
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA
+MFMA_F32_PEAK_TFS = 157.3   # MI355X dense fp32 MFMA
+
+WORKLOADS = {
+    "n4096": dict(kind="fp16", n_h=128, n=4096, desc="fp16 single sequence, n_h=128, N=4096 (BASELINE config 2)"),
+    "n65536": dict(kind="fp16", n_h=128, n=65536, desc="fp16 split-KV, n_h=128, N=65536 (BASELINE config 3)"),
+    "nh16": dict(kind="fp16", n_h=16, n=32768, desc="fp16 low-head, n_h=16, N=32768 (BASELINE config 4)"),
+    "batched": dict(kind="batched", n_h=128, batch=32,
+                    desc="fp16 batched, B=32, N_b ~ U[512,16384] seed 42 (BASELINE config 5)"),
+    "fp32": dict(kind="fp32", n_h=128, n=1024, desc="fp32 path, n_h=128, N=1024 (BASELINE config 1 shape on GPU)"),
+}
+
+
+def algorithmic(kind, n_h, total_tokens, batch=1):
+    """Bytes and flops of one call: e*(n_h*576 + N*576 + n_h*512), 2*n_h*N*1088."""
+    e = 4 if kind == "fp32" else 2
+    bytes_ = e * (batch * n_h * 576 + total_tokens * 576 + batch * n_h * 512)
+    flops = 2 * n_h * total_tokens * (576 + 512)
+    return bytes_, flops
+
+
+def cpu_info():
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model, os.cpu_count()
+
+
+def cpu_baseline(n_h, n, reps=5):
+    """The oracle's C restatement of run_mla_decode_cpu (cpu.cpp:5-61), contract
+    form (scale 1/sqrt(192), 512 value columns), fp32, one thread pinned to one
+    core: 1 warm-up + median of `reps` calls on the workload's shape."""
+    import numpy as np
+    from oracle import mla_oracle
+    from ada_mla import synthetic
+    q, c = synthetic.decode_inputs(n_h, n, seed=42, dtype=np.float32)
+    old = os.sched_getaffinity(0)
+    core = min(old)
+    os.sched_setaffinity(0, {core})
+    try:
+        mla_oracle.naive_cpu(q, c)
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            mla_oracle.naive_cpu(q, c)
+            times.append(time.perf_counter() - t0)
+        ref_us = None
+        if mla_oracle.reference_cpu_available():
+            mla_oracle.reference_cpu(q, c)
+            rt = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                mla_oracle.reference_cpu(q, c)
+                rt.append(time.perf_counter() - t0)
+            ref_us = statistics.median(rt) * 1e6
+    finally:
+        os.sched_setaffinity(0, old)
+    model, ncpu = cpu_info()
+    return {
+        "value": statistics.median(times) * 1e6,
+        "unit": "us/call",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"oracle/mla_naive_cpu.c (restatement of run_mla_decode_cpu, cpu.cpp:5-61), fp32, "
+                   f"n_h={n_h}, N={n}, scale 1/sqrt(192), 512 value columns; gcc -O2; 1 thread pinned to "
+                   f"core {core}; 1 warm-up + median of {reps} calls; host: {model}, {ncpu} logical CPUs"),
+        "reference_binary_us": ref_us,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="n4096", choices=sorted(WORKLOADS))
+    ap.add_argument("--num-splits", type=int, default=0)
+    ap.add_argument("--flush-mb", type=int, default=1024)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the decode path is built and measured on "
+              "one MI355X; a multi-GPU figure is not produced). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from ada_mla import capi
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = capi.load()
+    wl = WORKLOADS[args.workload]
+    kind, n_h = wl["kind"], wl["n_h"]
+    stream = torch.cuda.current_stream(dev)
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+
+    if kind == "batched":
+        from ada_mla import synthetic
+        seqlens = synthetic.batched_seqlens(wl["batch"], seed=42)
+        batch = wl["batch"]
+        total = int(seqlens.sum())
+        cu = torch.zeros(batch + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(torch.from_numpy(seqlens), 0)
+        cu_d = cu.to(dev)
+        q_shape, c_shape = (batch, n_h, 576), (total, 576)
+        dtype = torch.float16
+    else:
+        batch, total = 1, wl["n"]
+        q_shape, c_shape = (n_h, 576), (total, 576)
+        dtype = torch.float32 if kind == "fp32" else torch.float16
+    esz = 4 if dtype == torch.float32 else 2
+    pair_bytes = (math.prod(q_shape) + math.prod(c_shape)) * esz
+    pool = max(2, math.ceil(args.flush_mb * 2**20 / pair_bytes))
+    qs = [torch.randn(q_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
+    cs = [torch.randn(c_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
+    out = torch.empty((batch, n_h, 512) if kind == "batched" else (n_h, 512), device=dev, dtype=dtype)
+
+    splits = args.num_splits
+    if kind == "fp16":
+        ws_bytes = lib.mla_decode_split_workspace_size(n_h, total, splits)
+        eff_splits = lib.mla_decode_split_num_splits(n_h, total, splits)
+    elif kind == "fp32":
+        ws_bytes = lib.mla_decode_fused_workspace_size(n_h, total, splits)
+        eff_splits = None
+    else:
+        ws_bytes = lib.mla_decode_split_batched_workspace_size(batch, n_h, total, splits)
+        eff_splits = None
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+
+    def check(st, fn):
+        if st != 0:
+            raise capi.MlaError(fn, st)
+
+    def phase1(i):
+        q, c = qs[i % pool], cs[i % pool]
+        if kind == "fp16":
+            check(lib.mla_decode_split_fp16_partials(q.data_ptr(), c.data_ptr(), ws.data_ptr(), ws_bytes,
+                                                     n_h, total, splits, 0, sptr), "partials")
+        elif kind == "fp32":
+            check(lib.mla_decode_fused_fp32(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                                            n_h, 576, total, splits, sptr), "fused_fp32")
+        else:
+            check(lib.mla_decode_split_batched_fp16(q.data_ptr(), c.data_ptr(), cu_d.data_ptr(), out.data_ptr(),
+                                                    ws.data_ptr(), ws_bytes, batch, n_h, total, splits, sptr),
+                  "batched")
+
+    def phase2():
+        if kind == "fp16":
+            check(lib.mla_decode_split_fp16_combine(ws.data_ptr(), ws_bytes, out.data_ptr(), n_h, total, splits,
+                                                    sptr), "combine")
+
+    for i in range(args.warmup):
+        phase1(i)
+        phase2()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    # (1) the timed region: exactly K steps, nothing but the decode calls
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(K):
+        phase1(args.warmup + i)
+        phase2()
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    us_call = total_ms * 1000.0 / K
+
+    # (2) the dominant kernel alone: an event pair around each split-kernel
+    # launch on the launch stream (the combine runs outside the pairs)
+    ka = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    kb = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    torch.cuda.synchronize()
+    for i in range(K):
+        ka[i].record(stream)
+        phase1(args.warmup + K + i)
+        kb[i].record(stream)
+        phase2()
+    torch.cuda.synchronize()
+    k_times = sorted(a.elapsed_time(b) * 1000.0 for a, b in zip(ka, kb))
+    k_us = statistics.mean(k_times)
+
+    alg_bytes, alg_flops = algorithmic(kind, n_h, total, batch)
+    achieved = alg_bytes / (k_us * 1e-6) / 1e9
+    mfma_peak = MFMA_F32_PEAK_TFS if kind == "fp32" else MFMA_F16_PEAK_TFS
+    tflops = alg_flops / (k_us * 1e-6) / 1e12
+    bound_hbm = alg_bytes / HBM_PEAK_GBS / 1e3  # us
+    bound_mfma = alg_flops / mfma_peak / 1e6    # us
+    if bound_hbm >= bound_mfma:
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS}
+    else:
+        roof = {"bound": "mfma", "achieved": tflops, "peak": mfma_peak, "unit": "TFLOP/s",
+                "frac": tflops / mfma_peak}
+    roof.update({
+        "traffic": None,
+        "kernel": "splitkv_fp16_kernel" if kind in ("fp16", "batched") else "splitkv_fp32_kernel",
+        "kernel_us": k_us,
+        "kernel_us_median": statistics.median(k_times),
+        "algorithmic_bytes": alg_bytes,
+        "algorithmic_flops": alg_flops,
+        "mfma_tflops": tflops,
+        "mfma_frac": tflops / mfma_peak,
+        "roofline_time_us": max(bound_hbm, bound_mfma),
+        "call_frac": max(bound_hbm, bound_mfma) / us_call,
+    })
+    if kind == "batched":
+        roof["note"] = "batched has no phase split: kernel_us is the whole call"
+
+    res = {
+        "metric": METRIC,
+        "value": us_call,
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": total_ms / K,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32" if kind == "fp32" else "fp16",
+        "data": "synthetic (N(0,1), torch generator seed 42, resident in HBM)",
+        "config": {
+            "workload": wl["desc"],
+            "num_heads": n_h,
+            "seq_len": total if kind != "batched" else None,
+            "total_tokens": total,
+            "batch": batch,
+            "num_splits": eff_splits,
+            "cache_flush": f"{pool} distinct (Q*, C) buffers, {pool * pair_bytes / 2**20:.0f} MB, rotated per step",
+            "parallelism": "single GPU",
+        },
+        "tbps": alg_bytes / (us_call * 1e-6) / 1e12,
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        cn = 1024 if kind == "fp32" else (total if kind == "fp16" else 4096)
+        res["cpu_baseline"] = cpu_baseline(n_h, cn)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -54,6 +54,12 @@ const char *mla_status_string(int status);
 /* hipError_t of the last failed HIP call on this thread (0 if none). */
 int mla_last_hip_error(void);
 
+/* Number of splits (partial results per head) that mla_decode_split_fp16
+ * uses for these arguments on the current device; 0 for invalid sizes.
+ * Replaces the fixed `num_splits = 4` of mla_decode_split
+ * (csrc/mla_api.cpp:97). */
+int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits);
+
 /* Workspace for mla_decode_split_fp16 (fp32 split partials). Replaces the
  * splits_max / splits_sum / splits_out buffers that mla_decode_split_
  * allocates per call (csrc/mla_api.cpp:71-75). Returns 0 for invalid sizes. */
