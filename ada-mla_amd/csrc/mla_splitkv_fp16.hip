@@ -270,20 +270,40 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                     const int blk = t + 1;
                     const int t0 = p_lo + blk * T::kBT;
                     const _Float16 *cs = s_ring + (blk % T::kRing) * T::kSlot;
-                    // ---- S^T tiles: tokens t0 + 16*tt + (0..15), heads 16*hg + (0..15)
+                    // ---- S^T tiles: tokens t0 + 16*tt + (0..15), heads 16*hg + (0..15).
+                    // The 36 operand reads go out in batches of 3 K-steps one
+                    // batch ahead of the MFMAs that consume them.
                     floatx4 acc[2][T::kChains];
 #pragma unroll
                     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                         for (int j = 0; j < T::kChains; ++j)
                             acc[tt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    constexpr int kB = 3;  // K-steps per batch
+                    half8 ab[2][kB][2];
+                    auto load_batch = [&](int buf, int k0) {
 #pragma unroll
-                    for (int kk = 0; kk < kDK / 32; ++kk)
+                        for (int k = 0; k < kB; ++k)
 #pragma unroll
-                        for (int tt = 0; tt < 2; ++tt)
-                            acc[tt][kk % T::kChains] = mfma16x16x32(
-                                *(const half8 *)(cs + (16 * tt + l16) * kDK + a_chunk(kk)), qf[kk],
-                                acc[tt][kk % T::kChains]);
+                            for (int tt = 0; tt < 2; ++tt)
+                                ab[buf][k][tt] = *(const half8 *)(cs + (16 * tt + l16) * kDK + a_chunk(k0 + k));
+                    };
+                    load_batch(0, 0);
+#pragma unroll
+                    for (int kb = 0; kb < kDK / 32 / kB; ++kb) {
+                        if (kb + 1 < kDK / 32 / kB)
+                            load_batch((kb + 1) & 1, (kb + 1) * kB);
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int k = 0; k < kB; ++k)
+#pragma unroll
+                            for (int tt = 0; tt < 2; ++tt) {
+                                const int kk = kb * kB + k;
+                                acc[tt][kk % T::kChains] =
+                                    mfma16x16x32(ab[kb & 1][k][tt], qf[kk], acc[tt][kk % T::kChains]);
+                            }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                     // ---- online softmax over the block for this wave's heads
                     float sv[2][4];
                     float mx = -INFINITY;
@@ -363,14 +383,15 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                             for (int dt = 0; dt < 8; ++dt)
                                 o[hs][dt] *= alpha[hs];
                     }
-                    // ---- O^T[dims 128*ow .. +128][heads] += C_N^T P^T
+                    // ---- O^T[dims 128*ow .. +128][heads] += C_N^T P^T. All 20
+                    // operand reads are issued before the 32 MFMAs.
                     half8 pb[T::kNHS];
 #pragma unroll
                     for (int hs = 0; hs < T::kNHS; ++hs)
                         pb[hs] = *(const half8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
+                    half8 av[8];
 #pragma unroll
                     for (int dt = 0; dt < 8; ++dt) {
-                        half8 a;
                         if constexpr (kTr) {
                             // lane (g, j): rows 8g + j/4 (+4), dims 128*ow + 16*dt + 4*(j%4) .. +3
                             const int r0 = 8 * g + (l16 >> 2);
@@ -380,19 +401,23 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                             const _Float16 *p1 = cs + (r0 + 4) * kDK + 8 * phys_chunk(cl, row_swizzle(r0 + 4)) + sub;
                             const half4 lo4 = lds_read_tr16(p0);
                             const half4 hi4 = lds_read_tr16(p1);
-                            a = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                            av[dt] = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
                         } else {
                             const int col = 128 * ow + 16 * dt + l16;
 #pragma unroll
                             for (int j = 0; j < 8; ++j) {
                                 const int r = 8 * g + j;
-                                a[j] = cs[r * kDK + 8 * phys_chunk(col >> 3, row_swizzle(r)) + (col & 7)];
+                                av[dt][j] = cs[r * kDK + 8 * phys_chunk(col >> 3, row_swizzle(r)) + (col & 7)];
                             }
                         }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
                         for (int hs = 0; hs < T::kNHS; ++hs)
-                            o[hs][dt] = mfma16x16x32(a, pb[hs], o[hs][dt]);
-                    }
+                            o[hs][dt] = mfma16x16x32(av[dt], pb[hs], o[hs][dt]);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
                 // ---- block t+2 (the S waves' next-but-one) must have landed
                 // before the barrier; block t+3 may stay in flight
