@@ -38,7 +38,7 @@ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // Smallest token count worth a split of its own: below this the fp32
 // partial write-back ([num_heads x 512] floats per split) outweighs the C
 // bytes the split reads.
-constexpr int kMinSplitTokensF16 = 256;
+constexpr int kMinSplitTokensF16 = 128;
 constexpr int kMinSplitTokensF32 = 64;
 
 constexpr size_t kAlign = 256;

@@ -8,41 +8,30 @@
 //  * fp32 partials; the max starts at -inf; an empty sequence writes zeros;
 //  * a sequence's slot range follows from the split plan (any number of
 //    splits, any batch);
-//  * one 256-thread workgroup per (head, 128-column quarter, sequence): lanes
-//    0..31 of each of 8 slot groups own 4 columns each and stream every 8th
-//    slot with independent 16-byte loads, so the partial reads of a head are
-//    spread over 4 workgroups and many loads are in flight per thread; the 8
-//    group sums are added through LDS.
+//  * one 512-thread workgroup per (16 x 16 output tile, sequence). The
+//    partial O is stored tile by tile in MFMA accumulator order
+//    (frag_offset), so a wave reads one slot's tile as 1 KB of contiguous
+//    memory; lane (g, h) owns head h, dims 4g..4g+3 of the tile. Each of the
+//    8 waves merges every 8th slot online (running max, rescaled sums) with
+//    the loads of the next 4 slots in flight while it merges the current 4,
+//    and the 8 wave results are merged through LDS.
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
 
 namespace mla {
 namespace {
 
-constexpr int kCols = 128;                 // output columns per workgroup
-constexpr int kQuads = kCols / 4;          // 32 threads per slot group
-constexpr int kGroups = 256 / kQuads;      // 8 slot groups
+constexpr int kWaves = 8;
+constexpr int kU = 4;  // slots per load batch and wave
 
-// Workgroup-wide reduction of one float (max or sum) over 256 threads.
-template <bool kMax>
-__device__ __forceinline__ float block_reduce(float v, float *red)
-{
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float o = __shfl_xor(v, off, 64);
-        v = kMax ? fmaxf(v, o) : v + o;
-    }
-    const int wave = threadIdx.x >> 6;
-    __syncthreads();  // red is reused
-    if ((threadIdx.x & 63) == 0)
-        red[wave] = v;
-    __syncthreads();
-    return kMax ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]))
-                : (red[0] + red[1]) + (red[2] + red[3]);
-}
+struct SlotBatch {
+    floatx4 v[kU];
+    float m[kU];
+    float l[kU];
+};
 
 template <bool kOutF32>
-__global__ __launch_bounds__(256)
+__global__ __launch_bounds__(64 * kWaves)
 void combine_kernel(const float *__restrict__ o_part,
                     const float *__restrict__ m_part,
                     const float *__restrict__ l_part,
@@ -50,63 +39,108 @@ void combine_kernel(const float *__restrict__ o_part,
                     void *__restrict__ out,
                     int num_heads, int total_tokens, int chunk)
 {
-    __shared__ float red[4];
-    __shared__ floatx4 part[kGroups][kQuads];
+    __shared__ float s_m[kWaves][64];
+    __shared__ float s_l[kWaves][64];
+    __shared__ floatx4 s_o[kWaves][64];
 
-    const int head = blockIdx.x;
-    const int col0 = blockIdx.y * kCols;
-    const int b = blockIdx.z;
-    const int tid = threadIdx.x;
-    const int quad = tid % kQuads;
-    const int grp = tid / kQuads;
+    const int tile = blockIdx.x;  // (head / 16) * 32 + dim / 16
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int head = (tile >> 5) * 16 + (lane & 15);
+    const int dim0 = (tile & 31) * 16 + 4 * (lane >> 4);
 
     int lo = 0, hi = total_tokens;
     if (cu_seqlens) {
         lo = min(max(cu_seqlens[b], 0), total_tokens);
         hi = min(max(cu_seqlens[b + 1], lo), total_tokens);
     }
+    float m = -INFINITY, l = 0.f;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    float inv_l = 0.f;
     if (hi > lo) {  // uniform per workgroup
         const int s0 = lo / chunk + b;
         const int ns = (hi - 1) / chunk + b - s0 + 1;
-        const float *mrow = m_part + (size_t)s0 * num_heads + head;
-        const float *lrow = l_part + (size_t)s0 * num_heads + head;
+        const size_t slot_floats = (size_t)num_heads * kDV;
+        const float *op = o_part + (size_t)s0 * slot_floats + (size_t)tile * 256 + lane * 4;
+        const float *mp = m_part + (size_t)s0 * num_heads + head;
+        const float *lp = l_part + (size_t)s0 * num_heads + head;
 
-        float mx = -INFINITY;
-        for (int s = tid; s < ns; s += 256)
-            mx = fmaxf(mx, mrow[(size_t)s * num_heads]);
-        const float m = block_reduce<true>(mx, red);
-        float ls = 0.f;
-        for (int s = tid; s < ns; s += 256)
-            ls += fast_exp2(mrow[(size_t)s * num_heads] - m) * lrow[(size_t)s * num_heads];
-        inv_l = 1.0f / block_reduce<false>(ls, red);
-
-        const float *orow = o_part + ((size_t)s0 * num_heads + head) * kDV + col0 + 4 * quad;
-        const size_t ostride = (size_t)num_heads * kDV;
-        int s = grp;
-        for (; s + 3 * kGroups < ns; s += 4 * kGroups) {
-            const floatx4 v0 = *(const floatx4 *)(orow + (size_t)s * ostride);
-            const floatx4 v1 = *(const floatx4 *)(orow + (size_t)(s + kGroups) * ostride);
-            const floatx4 v2 = *(const floatx4 *)(orow + (size_t)(s + 2 * kGroups) * ostride);
-            const floatx4 v3 = *(const floatx4 *)(orow + (size_t)(s + 3 * kGroups) * ostride);
-            acc += fast_exp2(mrow[(size_t)s * num_heads] - m) * v0;
-            acc += fast_exp2(mrow[(size_t)(s + kGroups) * num_heads] - m) * v1;
-            acc += fast_exp2(mrow[(size_t)(s + 2 * kGroups) * num_heads] - m) * v2;
-            acc += fast_exp2(mrow[(size_t)(s + 3 * kGroups) * num_heads] - m) * v3;
-        }
-        for (; s < ns; s += kGroups)
-            acc += fast_exp2(mrow[(size_t)s * num_heads] - m) * *(const floatx4 *)(orow + (size_t)s * ostride);
-    }
-    part[grp][quad] = acc;
-    __syncthreads();
-    if (grp == 0) {
-        floatx4 t = part[0][quad];
+        // slots k0, k0 + 8, ..., k0 + 8 (kU - 1) of this wave
+        auto load = [&](SlotBatch &sb, int k0) {
 #pragma unroll
-        for (int k = 1; k < kGroups; ++k)
-            t += part[k][quad];
-        t *= inv_l;
-        const size_t o_off = ((size_t)b * num_heads + head) * kDV + col0 + 4 * quad;
+            for (int j = 0; j < kU; ++j) {
+                const int s = k0 + kWaves * j;
+                if (s < ns) {
+                    sb.v[j] = *(const floatx4 *)(op + (size_t)s * slot_floats);
+                    sb.m[j] = mp[(size_t)s * num_heads];
+                    sb.l[j] = lp[(size_t)s * num_heads];
+                } else {
+                    sb.v[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    sb.m[j] = -INFINITY;
+                    sb.l[j] = 0.f;
+                }
+            }
+        };
+        auto merge = [&](const SlotBatch &sb) {
+            float mx = m;
+#pragma unroll
+            for (int j = 0; j < kU; ++j)
+                mx = fmaxf(mx, sb.m[j]);
+            if (mx != -INFINITY) {  // uniform per wave: the first batch holds a slot
+                const float sc = fast_exp2(m - mx);
+                acc *= sc;
+                l *= sc;
+#pragma unroll
+                for (int j = 0; j < kU; ++j) {
+                    const float e = fast_exp2(sb.m[j] - mx);
+                    acc += e * sb.v[j];
+                    l += e * sb.l[j];
+                }
+                m = mx;
+            }
+        };
+        constexpr int kStep = kWaves * kU;
+        SlotBatch A, B;
+        int k0 = w;
+        load(A, k0);
+        while (true) {
+            bool more = k0 + kStep < ns;
+            if (more)
+                load(B, k0 + kStep);
+            merge(A);
+            if (!more)
+                break;
+            k0 += kStep;
+            more = k0 + kStep < ns;
+            if (more)
+                load(A, k0 + kStep);
+            merge(B);
+            if (!more)
+                break;
+            k0 += kStep;
+        }
+    }
+    s_m[w][lane] = m;
+    s_l[w][lane] = l;
+    s_o[w][lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+        float mm = s_m[0][lane];
+#pragma unroll
+        for (int k = 1; k < kWaves; ++k)
+            mm = fmaxf(mm, s_m[k][lane]);
+        floatx4 t = {0.f, 0.f, 0.f, 0.f};
+        if (mm != -INFINITY) {
+            float ls = 0.f;
+#pragma unroll
+            for (int k = 0; k < kWaves; ++k) {
+                const float e = fast_exp2(s_m[k][lane] - mm);
+                ls += e * s_l[k][lane];
+                t += e * s_o[k][lane];
+            }
+            t *= 1.0f / ls;
+        }
+        const size_t o_off = ((size_t)b * num_heads + head) * kDV + dim0;
         if constexpr (kOutF32) {
             *(floatx4 *)((float *)out + o_off) = t;
         } else {
@@ -121,7 +155,7 @@ void combine_kernel(const float *__restrict__ o_part,
 hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
                           bool out_fp32, hipStream_t s)
 {
-    const dim3 grid(pb.num_heads, kDV / kCols, pb.batch), block(256);
+    const dim3 grid(pb.num_heads / 16 * (kDV / 16), pb.batch), block(64 * kWaves);
     if (out_fp32)
         hipLaunchKernelGGL(combine_kernel<true>, grid, block, 0, s, w.o, w.m, w.l,
                            pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk);

@@ -44,19 +44,41 @@ __device__ __forceinline__ float fast_exp2(float x)
     return __builtin_amdgcn_exp2f(x);
 }
 
-// max / sum over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48).
+// max / sum over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48)
+// on the VALU lane-swap instructions of gfx950 (v_permlane32_swap,
+// v_permlane16_swap), so the reduction does not queue behind LDS traffic.
+// With both operands equal, permlane32_swap leaves halves {lo, lo} and
+// {hi, hi}; combining the two results gives every lane f(v[l], v[l ^ 32]).
+// permlane16_swap does the same for odd/even rows of 16 lanes.
+template <typename F>
+__device__ __forceinline__ float reduce_over_lane_groups(float v, F f)
+{
+    const unsigned u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = f(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const unsigned w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return f(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ __forceinline__ float max_over_lane_groups(float v)
 {
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
+    return reduce_over_lane_groups(v, [](float x, float y) { return fmaxf(x, y); });
 }
 
 __device__ __forceinline__ float sum_over_lane_groups(float v)
 {
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+    return reduce_over_lane_groups(v, [](float x, float y) { return x + y; });
+}
+
+// Offset (in floats) of O[head][dim] within one slot of the fp32 partial
+// output: 16 x 16 tiles (16 heads x 16 value dims) stored in the MFMA
+// accumulator order, lane (16 * g + head % 16) holding dims 4g .. 4g+3 of
+// the tile, so that one wave writes or reads a tile as 1 KB of contiguous
+// memory. Tiles are ordered [head / 16][dim / 16].
+__host__ __device__ __forceinline__ size_t frag_offset(int head, int dim)
+{
+    return ((size_t)(head >> 4) * 32 + (dim >> 4)) * 256 + (((dim & 15) >> 2) * 16 + (head & 15)) * 4 + (dim & 3);
 }
 
 }  // namespace mla

@@ -28,9 +28,10 @@ struct Plan {
     int xcd_remap;     // 1: the head tiles of one chunk share an XCD
 };
 
-// Partial results of the split kernels (fp32): O unnormalised
-// [n_slots][num_heads][512], running max in log2 units and running sum
-// [n_slots][num_heads].
+// Partial results of the split kernels (fp32): O unnormalised, n_slots
+// blocks of num_heads x 512 floats each stored as 16 x 16 tiles in MFMA
+// accumulator order (frag_offset in mla_device.hpp); running max in log2
+// units and running sum [n_slots][num_heads].
 struct Partials {
     float *o;
     float *m;

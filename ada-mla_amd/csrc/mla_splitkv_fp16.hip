@@ -9,20 +9,30 @@
 //  * 512 threads = 8 wave64s, one workgroup per CU, in two roles with one
 //    wave of each role on every SIMD, so that one role's LDS and softmax
 //    latencies hide behind the other role's MFMAs:
-//      - S waves (HT/16 of them) compute the logits and the online softmax
-//        of block t+1: S^T = C Q*^T on 16x16x32 MFMAs, each wave owning 16
-//        heads x 32 tokens over the full K = 576 (eight independent
-//        accumulation chains) with its Q* fragment resident in registers,
-//        so no wave needs another wave's logits;
+//      - S waves compute the logits and the online softmax of block t+1:
+//        S^T = C Q*^T on 16x16x32 MFMAs over the full K = 576. Wave
+//        (head group, token half) owns up to 32 heads x 16 tokens of each
+//        32-token block, with the Q* of its heads resident in registers, so
+//        each C row is read from LDS once per head group. Each wave keeps its
+//        own running max: the two token halves of a head agree on a common
+//        reference only in the O waves (below), so no wave waits for
+//        another's logits.
 //      - O waves (4) accumulate block t: O^T = C_N^T P^T, each owning 128
 //        output columns for all heads of the tile, with the C_N^T operand
-//        read from the ring slot by the LDS transpose read
-//        (ds_read_b64_tr_b16); they also feed the ring.
-//    P (fp16) and the rescale factors pass from S to O waves through a
+//        read by the LDS transpose read (ds_read_b64_tr_b16) one step ahead,
+//        between the MFMAs of the current block. Per head they take M = max
+//        of the two halves' running maxima, scale each half's P by
+//        2^(m_half - M) and the accumulator by 2^(M_old - M). They also feed
+//        the ring, with the global->LDS loads also placed between MFMAs.
+//    P (fp16) and the halves' maxima pass from S to O waves through a
 //    double-buffered LDS area; one workgroup barrier per block.
 //  * C streams through a 4-slot LDS ring of 32-token blocks filled by
-//    direct global->LDS loads (global_load_lds_dwordx4), two blocks ahead of
-//    the S waves; each block is read from LDS by both products.
+//    direct global->LDS loads (global_load_lds_dwordx4). Q* of the head tile
+//    comes first, through the top slots, so the S waves can load it into
+//    registers while blocks 0.. arrive; afterwards block t+4 is requested
+//    into the slot of block t as soon as step t begins (its C_N^T operand
+//    is already in registers by then). Each block is read from LDS by both
+//    products.
 //  * Online softmax in fp32 (log2 domain), running max started at -inf; the
 //    O rescale is skipped when no head's max moved (exact: the factor is 1).
 //  * Rows of a ring slot are XOR-swizzled in 16-byte chunks so that both the
@@ -31,6 +41,8 @@
 //  * Barriers are plain s_barrier after an LDS counter wait: the
 //    global->LDS loads are tracked with explicit vmcnt waits by the waves
 //    that issue them, so a barrier never drains the loads in flight.
+//  * The partial O is stored tile by tile in the MFMA accumulator order
+//    (frag_offset): every store instruction writes 1 KB of contiguous memory.
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
 
@@ -43,23 +55,23 @@ struct F16Tile {
     static constexpr int kThreads = 64 * kWaves;
     static constexpr int kBT = 32;                      // tokens per block
     static constexpr int kRing = 4;                     // LDS ring slots
-    static constexpr int kSWaves = HT / 16;             // S waves (16 heads each)
+    static constexpr int kSH = HT < 32 ? HT : 32;       // heads per S wave
+    static constexpr int kNS = kSH / 16;                // 16-head sub-tiles per S wave
+    static constexpr int kNHG = HT / kSH;               // head groups
+    static constexpr int kSWaves = 2 * kNHG;            // S waves: (head group, token half)
+    static constexpr int kChains = 8 / kNS;             // accumulation chains per sub-tile
     static constexpr int kOWave0 = 4;                   // O waves are 4..7
     static constexpr int kNHS = HT / 16;                // 16-head sub-tiles per tile
-    static constexpr int kChains = 4;                   // accumulation chains per S^T tile
     static constexpr int kSlot = kBT * kDK;             // halves per slot (36 KB)
     static constexpr int kUnits = kSlot * 2 / 1024;     // 1 KB load units per slot
     static constexpr int kLoadsPerWave = kUnits / 4;    // per O wave per block
     static constexpr int kPRow = kBT + 8;               // P row stride (halves)
     // Q* of the head tile is staged through the top ring slots at the start
     // of each piece (HT rows of 1152 bytes, swizzled like C rows).
-    static constexpr int kQUnits = HT * kDK * 2 / 1024;
-    static constexpr int kQLoadsPerWave = (kQUnits + 3) / 4;
-    static constexpr int kQSlots = (HT * kDK + kSlot - 1) / kSlot;
-    static constexpr int kPreBlocks = kRing - kQSlots;  // blocks issued with Q*
+    static constexpr int kQBlocks = (HT + kBT - 1) / kBT;
+    static constexpr int kPre = kRing - kQBlocks;       // blocks issued with Q*
     static_assert(kUnits % 4 == 0, "units per wave");
     static_assert(kSWaves <= kOWave0, "S waves");
-    static_assert(kQSlots >= 1 && kQSlots <= 2, "Q slots");
 };
 
 // XOR swizzle of the 16-byte chunk index within a 1152-byte row. Bits of the
@@ -124,7 +136,8 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
     using T = F16Tile<HT>;
     __shared__ __attribute__((aligned(1024))) _Float16 s_ring[T::kRing * T::kSlot];
     __shared__ __attribute__((aligned(16))) _Float16 s_p[2][HT * T::kPRow];
-    __shared__ float s_alpha[2][HT];
+    __shared__ float s_m[2][2][HT];  // [P buffer][token half][head]: running max of the half
+    __shared__ float s_l[2][HT];     // [token half][head]: running sum at the end of a piece
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -152,15 +165,10 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
     const int hi = min(lo + chunk, total_tokens);
     if (lo >= hi)
         return;
-
-    const bool s_wave = wave < T::kSWaves;   // logits + softmax of 16 heads
-    const bool o_wave = wave >= T::kOWave0;  // 128 output columns + ring loads
-    const int hg = s_wave ? wave : 0;        // S wave: its 16-head group
-    const int ow = wave - T::kOWave0;        // O wave: its column quarter
     const int head0 = ht * HT;
 
     // First sequence containing token lo (largest b with cu[b] <= lo).
-    int b = 0;
+    int b_first = 0;
     const int nseq = cu_seqlens ? batch : 1;
     if (cu_seqlens) {
         int l = 0, r = batch;
@@ -168,213 +176,302 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
             const int mid = (l + r) >> 1;
             if (cu_seqlens[mid] <= lo) l = mid; else r = mid;
         }
-        b = l;
+        b_first = l;
     }
-
-    // Per-lane chunk offsets of the S^T operand reads (rows 16*tt + l16,
-    // logical chunk 4*kk + g). For kk < 16 the swizzle permutes kk within
-    // aligned groups of 4 and g within 0..3, so four offsets plus immediates
-    // cover them; the rope chunks 64..71 have two more.
-    const int swz_a = row_swizzle(l16);
-    int a_off[6];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        a_off[j] = 8 * (4 * (j ^ (swz_a >> 2)) + ((g ^ swz_a) & 3));
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-        a_off[4 + j] = 8 * (64 + ((4 * j + g) ^ (swz_a & 7)));
-    auto a_chunk = [&](int kk) { return kk < 16 ? a_off[kk & 3] + 128 * (kk >> 2) : a_off[kk - 12]; };
-
-    for (; b < nseq; ++b) {
-        int seq_lo = 0, seq_hi = total_tokens;
-        if (cu_seqlens) {
-            seq_lo = min(max(cu_seqlens[b], 0), total_tokens);
-            seq_hi = min(max(cu_seqlens[b + 1], seq_lo), total_tokens);
-        }
-        if (seq_lo >= hi)
-            break;
-        const int p_lo = max(seq_lo, lo);
-        const int p_hi = min(seq_hi, hi);
-        if (p_lo >= p_hi)
-            continue;
-        const int slot_out = split + b;
-        const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
-
-        lds_barrier();  // the ring and the P / alpha buffers are reused from the previous piece
-
-        // Global -> LDS load of block `blk` into ring slot blk % kRing by the
-        // O waves. Load unit u (1 KB) = chunk positions [64u, 64u + 64) of
-        // the slot; lane l fetches the logical chunk stored at position
-        // 64u + l. Rows past the end of the piece re-read its last token
-        // (finite data, masked later); a block past the last one re-reads
-        // only that token.
-        auto issue_block = [&](int blk) {
-            const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
-            const int lim = p_hi - 1 - t0;
-            const _Float16 *base = c + (size_t)t0 * kDK;
-            _Float16 *slot = s_ring + (blk % T::kRing) * T::kSlot;
-#pragma unroll
-            for (int k = 0; k < T::kLoadsPerWave; ++k) {
-                const int u = ow + 4 * k;
-                const int pos = 64 * u + lane;
-                const int row = pos / 72;
-                const int pc = pos - 72 * row;
-                const int lc = phys_chunk(pc, row_swizzle(row));
-                global_to_lds16(base, (min(row, lim) * kDK + lc * 8) * 2, slot + u * 512);
+    // Calls body(b, p_lo, p_hi) for every non-empty piece [p_lo, p_hi) of
+    // sequence b inside this chunk. Every wave walks the same pieces and,
+    // per piece, passes the same number of barriers (nblk + 6).
+    auto for_each_piece = [&](auto &&body) {
+        for (int b = b_first; b < nseq; ++b) {
+            int seq_lo = 0, seq_hi = total_tokens;
+            if (cu_seqlens) {
+                seq_lo = min(max(cu_seqlens[b], 0), total_tokens);
+                seq_hi = min(max(cu_seqlens[b + 1], seq_lo), total_tokens);
             }
-        };
-
-        // Prologue: Q* rows of this head tile go to the top kQSlots ring
-        // slots (their blocks are not needed yet), blocks 0.. to the others;
-        // blocks 0..2 are always issued (past the last block as re-reads of
-        // the last token), so every wait count is a constant.
-        if (o_wave) {
-            const _Float16 *qbase = q + ((size_t)b * num_heads + head0) * kDK;
-            _Float16 *qslot = s_ring + T::kPreBlocks * T::kSlot;
-#pragma unroll
-            for (int k = 0; k < T::kQLoadsPerWave; ++k) {
-                const int u = min(ow + 4 * k, T::kQUnits - 1);
-                const int pos = 64 * u + lane;
-                const int row = pos / 72;
-                const int pc = pos - 72 * row;
-                global_to_lds16(qbase, (row * kDK + 8 * phys_chunk(pc, row_swizzle(row))) * 2,
-                                qslot + u * 512);
-            }
-#pragma unroll
-            for (int blk = 0; blk < T::kPreBlocks; ++blk)
-                issue_block(blk);
-            MLA_WAIT_VMCNT(T::kPreBlocks * T::kLoadsPerWave);  // Q* has landed
+            if (seq_lo >= hi)
+                break;
+            const int p_lo = max(seq_lo, lo);
+            const int p_hi = min(seq_hi, hi);
+            if (p_lo < p_hi)
+                body(b, p_lo, p_hi);
         }
-        lds_barrier();
+    };
 
-        // Each role runs its own copy of the step loop (t = -1 .. nblk-1,
-        // S waves on block t+1, O waves on block t) with the same sequence of
-        // barriers, so that the registers of one role (Q* fragments, logit
-        // accumulators) and of the other (O accumulators) can share space.
-        if (s_wave) {
-            // Q* fragment (B operand of S^T = C Q*^T): lane holds head
-            // 16*hg + l16 of the tile, dims 32*kk + 8*g .. +7.
-            half8 qf[kDK / 32];
+    // Each role runs its own piece loop and step loop (t = -1 .. nblk-1: S
+    // waves on block t+1, O waves on block t) with the same sequence of
+    // barriers, so that the registers of one role (Q* fragments, logit
+    // accumulators) and of the other (O accumulators) can share space and
+    // each role's set-up stays out of the other's instruction stream.
+    if (wave < T::kSWaves) {
+        const int hg = wave >> 1;  // head group
+        const int th = wave & 1;   // token half of each block
+        // Per-lane chunk offsets of the row-wise operand reads (row r with
+        // r % 16 == l16, logical chunk 4*kk + g). For kk < 16 the swizzle
+        // permutes kk within aligned groups of 4 and g within 0..3, so four
+        // offsets plus immediates cover them; the rope chunks 64..71 have two
+        // more.
+        const int swz_a = row_swizzle(l16);
+        int a_off[6];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            a_off[j] = 8 * (4 * (j ^ (swz_a >> 2)) + ((g ^ swz_a) & 3));
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            a_off[4 + j] = 8 * (64 + ((4 * j + g) ^ (swz_a & 7)));
+        auto a_chunk = [&](int kk) { return kk < 16 ? a_off[kk & 3] + 128 * (kk >> 2) : a_off[kk - 12]; };
+
+        for_each_piece([&](int b, int p_lo, int p_hi) {
+            const int slot_out = split + b;
+            const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
+            lds_barrier();  // piece start: buffers are reused from the previous piece
+            lds_barrier();  // A: Q* has landed in the top ring slots
+            // Q* fragments (B operand of S^T = C Q*^T): lane holds head
+            // kSH*hg + 16*ns + l16 of the tile, dims 32*kk + 8*g .. +7. Q*
+            // rows sit in the ring in the same swizzled layout as C rows.
+            half8 qf[T::kNS][kDK / 32];
             {
-                const _Float16 *qs = s_ring + T::kPreBlocks * T::kSlot + (16 * hg + l16) * kDK;
+                const _Float16 *qs = s_ring + T::kPre * T::kSlot + (T::kSH * hg + l16) * kDK;
 #pragma unroll
-                for (int kk = 0; kk < kDK / 32; ++kk)
-                    qf[kk] = *(const half8 *)(qs + a_chunk(kk));
+                for (int ns = 0; ns < T::kNS; ++ns)
+#pragma unroll
+                    for (int kk = 0; kk < kDK / 32; ++kk)
+                        qf[ns][kk] = *(const half8 *)(qs + 16 * ns * kDK + a_chunk(kk));
             }
-            lds_barrier();  // Q* slots are free again
-            lds_barrier();  // block 0 has landed
+            lds_barrier();  // B: the Q* slots are free again
+            lds_barrier();  // C: block 0 has landed
 
-            float m_run = -INFINITY, l_run = 0.f;  // head 16*hg + l16
+            float m_run[T::kNS], l_lane[T::kNS];  // running max (uniform over g); per-lane partial sum
+#pragma unroll
+            for (int ns = 0; ns < T::kNS; ++ns) {
+                m_run[ns] = -INFINITY;
+                l_lane[ns] = 0.f;
+            }
             for (int t = -1; t < nblk; ++t) {
                 if (t + 1 < nblk) {
                     const int blk = t + 1;
-                    const int t0 = p_lo + blk * T::kBT;
-                    const _Float16 *cs = s_ring + (blk % T::kRing) * T::kSlot;
-                    // ---- S^T tiles: tokens t0 + 16*tt + (0..15), heads 16*hg + (0..15).
-                    // The 36 operand reads go out in batches of 3 K-steps one
-                    // batch ahead of the MFMAs that consume them.
-                    floatx4 acc[2][T::kChains];
+                    const int t0 = p_lo + blk * T::kBT + 16 * th;
+                    const _Float16 *crow = s_ring + (blk % T::kRing) * T::kSlot + (16 * th + l16) * kDK;
+                    // ---- S^T tiles: tokens t0 + (0..15), heads of this wave.
+                    // The 18 operand reads go out in batches of 3 K-steps,
+                    // two batches ahead of the MFMAs that consume them.
+                    floatx4 acc[T::kNS][T::kChains];
 #pragma unroll
-                    for (int tt = 0; tt < 2; ++tt)
+                    for (int ns = 0; ns < T::kNS; ++ns)
 #pragma unroll
                         for (int j = 0; j < T::kChains; ++j)
-                            acc[tt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-                    constexpr int kB = 3;  // K-steps per batch
-                    half8 ab[2][kB][2];
+                            acc[ns][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    constexpr int kB = 3;                 // K-steps per batch
+                    constexpr int kNB = kDK / 32 / kB;    // batches (6)
+                    half8 ab[3][kB];
                     auto load_batch = [&](int buf, int k0) {
 #pragma unroll
                         for (int k = 0; k < kB; ++k)
-#pragma unroll
-                            for (int tt = 0; tt < 2; ++tt)
-                                ab[buf][k][tt] = *(const half8 *)(cs + (16 * tt + l16) * kDK + a_chunk(k0 + k));
+                            ab[buf][k] = *(const half8 *)(crow + a_chunk(k0 + k));
                     };
                     load_batch(0, 0);
+                    load_batch(1, kB);
 #pragma unroll
-                    for (int kb = 0; kb < kDK / 32 / kB; ++kb) {
-                        if (kb + 1 < kDK / 32 / kB)
-                            load_batch((kb + 1) & 1, (kb + 1) * kB);
+                    for (int bi = 0; bi < kNB; ++bi) {
+                        if (bi + 2 < kNB)
+                            load_batch((bi + 2) % 3, (bi + 2) * kB);
                         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                         for (int k = 0; k < kB; ++k)
 #pragma unroll
-                            for (int tt = 0; tt < 2; ++tt) {
-                                const int kk = kb * kB + k;
-                                acc[tt][kk % T::kChains] =
-                                    mfma16x16x32(ab[kb & 1][k][tt], qf[kk], acc[tt][kk % T::kChains]);
+                            for (int ns = 0; ns < T::kNS; ++ns) {
+                                const int kk = bi * kB + k;
+                                acc[ns][kk % T::kChains] =
+                                    mfma16x16x32(ab[bi % 3][k], qf[ns][kk], acc[ns][kk % T::kChains]);
                             }
                         __builtin_amdgcn_sched_barrier(0);
                     }
-                    // ---- online softmax over the block for this wave's heads
-                    float sv[2][4];
-                    float mx = -INFINITY;
+                    // ---- online softmax of this wave's 16 tokens, per head
 #pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
-                        const floatx4 st = (acc[tt][0] + acc[tt][1]) + (acc[tt][2] + acc[tt][3]);
+                    for (int ns = 0; ns < T::kNS; ++ns) {
+                        floatx4 st = acc[ns][0];
+#pragma unroll
+                        for (int j = 1; j < T::kChains; ++j)
+                            st += acc[ns][j];
+                        float sv[4];
+                        float mx = -INFINITY;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            const int tok = t0 + 16 * tt + 4 * g + i;
-                            sv[tt][i] = tok < p_hi ? st[i] * scale_log2 : -INFINITY;
-                            mx = fmaxf(mx, sv[tt][i]);
+                            sv[i] = (t0 + 4 * g + i) < p_hi ? st[i] * scale_log2 : -INFINITY;
+                            mx = fmaxf(mx, sv[i]);
                         }
-                    }
-                    mx = max_over_lane_groups(mx);
-                    const float mn = fmaxf(m_run, mx);
-                    const float alpha = fast_exp2(m_run - mn);
-                    m_run = mn;
-                    float psum = 0.f;
-                    _Float16 *prow = s_p[blk & 1] + (16 * hg + l16) * T::kPRow + 4 * g;
-#pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
+                        mx = max_over_lane_groups(mx);
+                        const float mn = fmaxf(m_run[ns], mx);
+                        // a half with no valid token yet keeps max -inf; its
+                        // exponents are taken against 0 so that they are 0
+                        const float ref = mn == -INFINITY ? 0.f : mn;
+                        const float alpha = fast_exp2(m_run[ns] - ref);
+                        m_run[ns] = mn;
                         half4 ph;
+                        float ps = 0.f;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            const float p = fast_exp2(sv[tt][i] - mn);
-                            psum += p;
+                            const float p = fast_exp2(sv[i] - ref);
+                            ps += p;
                             ph[i] = (_Float16)p;
                         }
-                        *(half4 *)(prow + 16 * tt) = ph;
+                        l_lane[ns] = l_lane[ns] * alpha + ps;
+                        const int hrow = T::kSH * hg + 16 * ns + l16;
+                        *(half4 *)(s_p[blk & 1] + hrow * T::kPRow + 16 * th + 4 * g) = ph;
+                        if (g == 0)
+                            s_m[blk & 1][th][hrow] = mn;
                     }
-                    l_run = l_run * alpha + psum;
-                    if (g == 0)
-                        s_alpha[blk & 1][16 * hg + l16] = alpha;
                 }
                 lds_barrier();
             }
-            // ---- epilogue: m and l of this wave's heads
-            const float ls = sum_over_lane_groups(l_run);
-            if (g == 0) {
-                m_part[(size_t)slot_out * num_heads + head0 + 16 * hg + l16] = m_run;
-                l_part[(size_t)slot_out * num_heads + head0 + 16 * hg + l16] = ls;
-            }
-        } else if (o_wave) {
-            lds_barrier();  // Q* slots are free again
+            // ---- epilogue: this half's running max and sum per head; the
+            // first half merges both and writes the piece's m and l
 #pragma unroll
-            for (int blk = T::kPreBlocks; blk < T::kRing - 1; ++blk)
-                issue_block(blk);
-            // block 0 has landed; blocks 1 and 2 may stay in flight
-            MLA_WAIT_VMCNT(2 * T::kLoadsPerWave);
+            for (int ns = 0; ns < T::kNS; ++ns) {
+                const float ls = sum_over_lane_groups(l_lane[ns]);
+                if (g == 0) {
+                    s_m[0][th][T::kSH * hg + 16 * ns + l16] = m_run[ns];
+                    s_l[th][T::kSH * hg + 16 * ns + l16] = ls;
+                }
+            }
             lds_barrier();
+            if (th == 0 && g == 0) {
+#pragma unroll
+                for (int ns = 0; ns < T::kNS; ++ns) {
+                    const int h = T::kSH * hg + 16 * ns + l16;
+                    const float m0 = s_m[0][0][h], m1 = s_m[0][1][h];
+                    const float mm = fmaxf(m0, m1);  // finite: the piece has a token
+                    const float ls = s_l[0][h] * fast_exp2(m0 - mm) + s_l[1][h] * fast_exp2(m1 - mm);
+                    m_part[(size_t)slot_out * num_heads + head0 + h] = mm;
+                    l_part[(size_t)slot_out * num_heads + head0 + h] = ls;
+                }
+            }
+        });
+    } else if (wave >= T::kOWave0) {
+        const int ow = wave - T::kOWave0;  // column quarter
+        // The O waves issue first when both waves of a SIMD are ready: their
+        // P reads at the start of a step then reach the LDS ahead of the S
+        // waves' operand reads, and their MFMAs carry the step.
+        __builtin_amdgcn_s_setprio(2);
+        // Global -> LDS load of unit u (1 KB) of a 32-row block whose row 0
+        // is at `base` into ring slot `slot`: chunk positions [64u, 64u + 64)
+        // of the slot, lane l fetching the logical chunk stored at position
+        // 64u + l. Rows past `lim` re-read row `lim` (finite data, masked
+        // later or never read).
+        // This wave's units are u = ow + 4k (k = 0..8); per unit, the lane's
+        // row (high half) and byte offset within the row (low half).
+        int unit_rc[T::kLoadsPerWave];
+#pragma unroll
+        for (int k = 0; k < T::kLoadsPerWave; ++k) {
+            const int pos = 64 * (ow + 4 * k) + lane;
+            const int row = pos / 72;
+            const int pc = pos - 72 * row;
+            unit_rc[k] = (row << 16) | (phys_chunk(pc, row_swizzle(row)) * 16);
+        }
+        auto load_unit = [&](const _Float16 *base, int lim, int slot, int k) {
+            const int off = min(unit_rc[k] >> 16, lim) * (kDK * 2) + (unit_rc[k] & 0xffff);
+            global_to_lds16(base, off, s_ring + slot * T::kSlot + (ow + 4 * k) * 512);
+        };
+        // C_N^T operand of dims 128*ow + 16*dt .. +15 from a ring slot
+        auto load_av = [&](const _Float16 *cs, int dt) -> half8 {
+            if constexpr (kTr) {
+                // lane (g, j): rows 8g + j/4 (+4), dims 128*ow + 16*dt + 4*(j%4) .. +3
+                const int r0 = 8 * g + (l16 >> 2);
+                const int cl = 16 * ow + 2 * dt + ((l16 & 3) >> 1);
+                const int sub = 4 * (l16 & 1);
+                const half4 lo4 = lds_read_tr16(cs + r0 * kDK + 8 * phys_chunk(cl, row_swizzle(r0)) + sub);
+                const half4 hi4 = lds_read_tr16(cs + (r0 + 4) * kDK + 8 * phys_chunk(cl, row_swizzle(r0 + 4)) + sub);
+                return half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            } else {
+                half8 v;
+                const int col = 128 * ow + 16 * dt + l16;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int r = 8 * g + j;
+                    v[j] = cs[r * kDK + 8 * phys_chunk(col >> 3, row_swizzle(r)) + (col & 7)];
+                }
+                return v;
+            }
+        };
+
+        for_each_piece([&](int b, int p_lo, int p_hi) {
+            const int slot_out = split + b;
+            const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
+            // unit k (0..8) of this wave's share of block blk; a block past
+            // the last re-reads the last token only
+            auto issue_unit = [&](int blk, int k) {
+                const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
+                load_unit(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk % T::kRing, k);
+            };
+            lds_barrier();  // piece start
+            // Prologue: Q* of the head tile into the top kQBlocks slots first
+            // (the S waves need it before any block), then blocks 0..kPre-1.
+            {
+                const _Float16 *qb = q + ((size_t)b * num_heads + head0) * kDK;
+#pragma unroll
+                for (int j = 0; j < T::kQBlocks; ++j)
+#pragma unroll
+                    for (int k = 0; k < T::kLoadsPerWave; ++k)
+                        load_unit(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, k);
+            }
+#pragma unroll
+            for (int blk = 0; blk < T::kPre; ++blk)
+#pragma unroll
+                for (int k = 0; k < T::kLoadsPerWave; ++k)
+                    issue_unit(blk, k);
+            MLA_WAIT_VMCNT(T::kPre * T::kLoadsPerWave);  // Q* has landed
+            lds_barrier();  // A
+            lds_barrier();  // B: the S waves hold Q* in registers
+#pragma unroll
+            for (int blk = T::kPre; blk < T::kRing; ++blk)
+#pragma unroll
+                for (int k = 0; k < T::kLoadsPerWave; ++k)
+                    issue_unit(blk, k);
+            MLA_WAIT_VMCNT((T::kRing - 1) * T::kLoadsPerWave);  // block 0 has landed
+            lds_barrier();  // C
 
             floatx4 o[T::kNHS][8];
+            float m_ref[T::kNHS];  // per head l16 of sub-tile hs: the accumulator's reference max
 #pragma unroll
-            for (int hs = 0; hs < T::kNHS; ++hs)
+            for (int hs = 0; hs < T::kNHS; ++hs) {
+                m_ref[hs] = -INFINITY;
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt)
                     o[hs][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+            // C_N^T fragments of the block the next step accumulates; each
+            // step reloads them for its successor right after the MFMAs that
+            // consume them
+            half8 av[8];
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt)
+                av[dt] = load_av(s_ring, dt);
 
             for (int t = -1; t < nblk; ++t) {
-                if (t >= 0 && t + T::kRing - 1 < nblk)
-                    issue_block(t + T::kRing - 1);  // into the slot block t-1 left
+                // block t+4 goes into the slot of block t, which every wave
+                // has finished reading (its C_N^T fragments are in av)
+                const bool issue = t >= 0 && t + T::kRing < nblk;
                 if (t >= 0) {
                     const int blk = t;
-                    const _Float16 *cs = s_ring + (blk % T::kRing) * T::kSlot;
-                    // ---- rescale, skipped when no head's max moved
+                    // ---- common reference max of the two token halves; P of
+                    // the half this lane feeds (tokens 8g..8g+7: half g/2) is
+                    // scaled onto it, the accumulator moves by 2^(M_old - M)
+                    half8 pb[T::kNHS];
+                    float m0[T::kNHS], m1[T::kNHS];
+#pragma unroll
+                    for (int hs = 0; hs < T::kNHS; ++hs) {
+                        m0[hs] = s_m[blk & 1][0][16 * hs + l16];
+                        m1[hs] = s_m[blk & 1][1][16 * hs + l16];
+                        pb[hs] = *(const half8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
+                    }
                     float alpha[T::kNHS];
                     bool moved = false;
 #pragma unroll
                     for (int hs = 0; hs < T::kNHS; ++hs) {
-                        alpha[hs] = s_alpha[blk & 1][16 * hs + l16];
+                        const float mn = fmaxf(m0[hs], m1[hs]);  // finite: token p_lo is in half 0
+                        alpha[hs] = fast_exp2(m_ref[hs] - mn);
                         moved |= alpha[hs] != 1.0f;
+                        m_ref[hs] = mn;
+                        pb[hs] *= (_Float16)fast_exp2((g < 2 ? m0[hs] : m1[hs]) - mn);
                     }
                     if (__builtin_amdgcn_ballot_w64(moved) != 0) {
 #pragma unroll
@@ -383,62 +480,45 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                             for (int dt = 0; dt < 8; ++dt)
                                 o[hs][dt] *= alpha[hs];
                     }
-                    // ---- O^T[dims 128*ow .. +128][heads] += C_N^T P^T. All 20
-                    // operand reads are issued before the 32 MFMAs.
-                    half8 pb[T::kNHS];
-#pragma unroll
-                    for (int hs = 0; hs < T::kNHS; ++hs)
-                        pb[hs] = *(const half8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
-                    half8 av[8];
+                    // ---- O^T[dims 128*ow .. +128][heads] += C_N^T P^T, with the
+                    // next block's operand reads and this step's global->LDS
+                    // loads placed between the MFMAs
+                    const _Float16 *cn = s_ring + ((blk + 1) % T::kRing) * T::kSlot;
 #pragma unroll
                     for (int dt = 0; dt < 8; ++dt) {
-                        if constexpr (kTr) {
-                            // lane (g, j): rows 8g + j/4 (+4), dims 128*ow + 16*dt + 4*(j%4) .. +3
-                            const int r0 = 8 * g + (l16 >> 2);
-                            const int cl = 16 * ow + 2 * dt + ((l16 & 3) >> 1);
-                            const int sub = 4 * (l16 & 1);
-                            const _Float16 *p0 = cs + r0 * kDK + 8 * phys_chunk(cl, row_swizzle(r0)) + sub;
-                            const _Float16 *p1 = cs + (r0 + 4) * kDK + 8 * phys_chunk(cl, row_swizzle(r0 + 4)) + sub;
-                            const half4 lo4 = lds_read_tr16(p0);
-                            const half4 hi4 = lds_read_tr16(p1);
-                            av[dt] = half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-                        } else {
-                            const int col = 128 * ow + 16 * dt + l16;
-#pragma unroll
-                            for (int j = 0; j < 8; ++j) {
-                                const int r = 8 * g + j;
-                                av[dt][j] = cs[r * kDK + 8 * phys_chunk(col >> 3, row_swizzle(r)) + (col & 7)];
-                            }
-                        }
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
                         for (int hs = 0; hs < T::kNHS; ++hs)
                             o[hs][dt] = mfma16x16x32(av[dt], pb[hs], o[hs][dt]);
-                    __builtin_amdgcn_sched_barrier(0);
+                        av[dt] = load_av(cn, dt);
+                        if (issue)
+                            issue_unit(blk + T::kRing, dt);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    if (issue)
+                        issue_unit(blk + T::kRing, 8);
                 }
-                // ---- block t+2 (the S waves' next-but-one) must have landed
-                // before the barrier; block t+3 may stay in flight
-                if (t >= 0 && t + T::kRing - 1 < nblk) MLA_WAIT_VMCNT(T::kLoadsPerWave);
+                // ---- block t+2 (the S waves' next) must have landed before
+                // the barrier; blocks t+3 and t+4 may stay in flight
+                if (t < 0 || issue) MLA_WAIT_VMCNT(2 * T::kLoadsPerWave);
                 else MLA_WAIT_VMCNT(0);
                 lds_barrier();
             }
-            // ---- epilogue: the unnormalised O of this piece
-            float *obase = o_part + ((size_t)slot_out * num_heads + head0 + l16) * kDV + 128 * ow + 4 * g;
+            lds_barrier();  // epilogue barrier of the S waves
+            // ---- epilogue: the unnormalised O of this piece, tile by tile
+            float *obase = o_part + (size_t)slot_out * num_heads * kDV + lane * 4;
 #pragma unroll
             for (int hs = 0; hs < T::kNHS; ++hs)
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt)
-                    *(floatx4 *)(obase + 16 * hs * kDV + 16 * dt) = o[hs][dt];
-        } else {
-            // waves with no role at this head-tile size keep the barrier count
-            lds_barrier();
-            lds_barrier();
-            for (int t = -1; t < nblk; ++t)
+                    *(floatx4 *)(obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt)) = o[hs][dt];
+        });
+    } else {
+        // waves with no role at this head-tile size keep the barrier count
+        for_each_piece([&](int, int p_lo, int p_hi) {
+            const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
+            for (int i = 0; i < nblk + 6; ++i)
                 lds_barrier();
-        }
+        });
     }
 }
 

@@ -215,10 +215,11 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
             m_part[(size_t)slot * num_heads + head0 + tid] = m_run;
             l_part[(size_t)slot * num_heads + head0 + tid] = lsum;
         }
-        float *orow = o_part + ((size_t)slot * num_heads + head0 + l16) * kDV + 128 * wave + 4 * g;
+        // tile by tile in MFMA accumulator order: 1 KB of contiguous memory per store
+        float *obase = o_part + (size_t)slot * num_heads * kDV + lane * 4;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
-            *(floatx4 *)(orow + 16 * dt) = o[dt];
+            *(floatx4 *)(obase + frag_offset(head0, 128 * wave + 16 * dt)) = o[dt];
     }
 }
 

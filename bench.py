@@ -120,6 +120,9 @@ def main():
     ap.add_argument("--num-splits", type=int, default=0)
     ap.add_argument("--flush-mb", type=int, default=1024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                    help="run 10 plain device-to-device copies of MB MiB instead of the decode: the "
+                         "known-size kernel that scales rocprof's FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -135,6 +138,21 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        n = args.calibrate_copy * 2**20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(10):
+            dst.copy_(src)
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 100.0
+        print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "us_per_copy": us,
+                          "GBps_read_plus_write": 2 * n / (us * 1e-6) / 1e9}), flush=True)
+        return
     lib = capi.load()
     wl = WORKLOADS[args.workload]
     kind, n_h = wl["kind"], wl["n_h"]
