@@ -35,10 +35,8 @@ int current_cu_count()
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-// Smallest token count worth a split of its own: below this the fp32
-// partial write-back ([num_heads x 512] floats per split) outweighs the C
-// bytes the split reads.
-constexpr int kMinSplitTokensF16 = 128;
+// fp32 path: smallest token count worth a split of its own (below it the
+// fp32 partial write-back outweighs the C bytes the split reads).
 constexpr int kMinSplitTokensF32 = 64;
 
 constexpr size_t kAlign = 256;
@@ -61,42 +59,92 @@ int fail_hip(hipError_t e)
 
 }  // namespace
 
+namespace {
+
+// Chunking of total_tokens into about `w` chunks of whole blocks.
+void set_chunks(Plan &p, int total_tokens, int batch, int w)
+{
+    w = std::max(1, std::min(w, ceil_div(total_tokens, p.block_tokens)));
+    p.chunk = ceil_div(ceil_div(total_tokens, w), p.block_tokens) * p.block_tokens;
+    p.n_chunks = ceil_div(total_tokens, p.chunk);
+    p.n_slots = p.n_chunks + batch - 1;
+    p.xcd_remap = (p.n_chunks % 8 == 0) ? 1 : 0;
+}
+
+// Modelled time of one fp16 decode call (us) for a plan, fitted to MI355X
+// measurements of this library: a fixed cost per call (two launches, the
+// prologue, the partial store), one 32-token step per block plus one, at a
+// step time that grows with the head tile (64: 1.5 us, 32: 0.88 us, 16:
+// 0.65 us with every CU busy), the partial traffic (written, then read by
+// the combine) at ~8 TB/s and the combine's memory round trips. Head tiles
+// that share a chunk but not an XCD re-read C from HBM, which the model
+// charges as slower steps.
+double modelled_us(const Plan &p, int num_heads, int batch, int cu_count)
+{
+    const double step_us = p.head_tile == 64 ? 1.5 : p.head_tile == 32 ? 0.88 : 0.65;
+    const int wgs = p.n_chunks * p.n_head_tiles;
+    const double rounds = std::ceil((double)wgs / cu_count);
+    const double steps = std::ceil((double)p.chunk / p.block_tokens) + 1.0;
+    const double share = (p.n_head_tiles > 1 && !p.xcd_remap) ? 1.3 : 1.0;
+    const double partial_bytes = (double)p.n_slots * num_heads * (kDV + 2) * 4.0;
+    // the combine merges up to 128 slots of a tile per memory round trip
+    const double slots_per_seq = std::ceil((double)p.n_slots / batch);
+    const double combine_trips = std::ceil(slots_per_seq / 128.0);
+    return 11.0 + rounds * steps * step_us * share + 2.0 * partial_bytes / 8.0e6 + 1.0 * combine_trips;
+}
+
+}  // namespace
+
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
                int num_splits, int cu_count)
 {
     Plan p{};
-    if (fp32) {
-        p.head_tile = 16;
-        p.block_tokens = 16;
-    } else {
-        p.head_tile = (num_heads % 64 == 0) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
-        p.block_tokens = 32;
-    }
-    p.n_head_tiles = num_heads / p.head_tile;
-    const int wgs_per_cu = 1;
     if (total_tokens <= 0) {
+        p.head_tile = fp32 ? 16 : (num_heads % 64 == 0) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
+        p.block_tokens = fp32 ? 16 : 32;
+        p.n_head_tiles = num_heads / p.head_tile;
         p.chunk = p.block_tokens;
         p.n_chunks = 0;
         p.n_slots = batch;  // unused; keeps the workspace non-empty
         p.xcd_remap = 0;
         return p;
     }
-    int w;
-    if (num_splits > 0) {
-        w = num_splits;
-    } else {
-        w = (cu_count * wgs_per_cu) / p.n_head_tiles;
-        const int min_tok = fp32 ? kMinSplitTokensF32 : kMinSplitTokensF16;
-        w = std::min(w, ceil_div(total_tokens, min_tok));
-        if (w < 1)
-            w = 1;
+    if (fp32) {
+        p.head_tile = 16;
+        p.block_tokens = 16;
+        p.n_head_tiles = num_heads / p.head_tile;
+        int w = num_splits;
+        if (w <= 0)
+            w = std::min(cu_count / p.n_head_tiles, ceil_div(total_tokens, kMinSplitTokensF32));
+        set_chunks(p, total_tokens, batch, w);
+        return p;
     }
-    w = std::min(w, ceil_div(total_tokens, p.block_tokens));
-    p.chunk = ceil_div(ceil_div(total_tokens, w), p.block_tokens) * p.block_tokens;
-    p.n_chunks = ceil_div(total_tokens, p.chunk);
-    p.n_slots = p.n_chunks + batch - 1;
-    p.xcd_remap = (p.n_chunks % 8 == 0) ? 1 : 0;
-    return p;
+    // fp16: the head tile (64, 32 or 16 heads per workgroup) and the split
+    // count with the smallest modelled call time, at most one workgroup per
+    // CU; a requested split count fixes the chunking and only the tile is
+    // chosen.
+    Plan best{};
+    double best_us = 0.0;
+    for (int ht : {64, 32, 16}) {
+        if (num_heads % ht != 0)
+            continue;
+        Plan c{};
+        c.head_tile = ht;
+        c.block_tokens = 32;
+        c.n_head_tiles = num_heads / ht;
+        int w_lo = 1, w_hi = std::max(1, std::min(cu_count / c.n_head_tiles, ceil_div(total_tokens, c.block_tokens)));
+        if (num_splits > 0)
+            w_lo = w_hi = num_splits;
+        for (int w = w_lo; w <= w_hi; ++w) {
+            set_chunks(c, total_tokens, batch, w);
+            const double us = modelled_us(c, num_heads, batch, cu_count);
+            if (best_us == 0.0 || us < best_us) {
+                best = c;
+                best_us = us;
+            }
+        }
+    }
+    return best;
 }
 
 size_t partials_bytes(const Plan &p, int num_heads)

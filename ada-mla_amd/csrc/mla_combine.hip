@@ -13,8 +13,9 @@
 //    (frag_offset), so a wave reads one slot's tile as 1 KB of contiguous
 //    memory; lane (g, h) owns head h, dims 4g..4g+3 of the tile. Each of the
 //    8 waves merges every 8th slot online (running max, rescaled sums) with
-//    the loads of the next 4 slots in flight while it merges the current 4,
-//    and the 8 wave results are merged through LDS.
+//    the loads of the next 8 slots in flight while it merges the current 8
+//    (128 slots per memory round trip), and the 8 wave results are merged
+//    through LDS.
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
 
@@ -22,7 +23,7 @@ namespace mla {
 namespace {
 
 constexpr int kWaves = 8;
-constexpr int kU = 4;  // slots per load batch and wave
+constexpr int kU = 8;  // slots per load batch and wave
 
 struct SlotBatch {
     floatx4 v[kU];

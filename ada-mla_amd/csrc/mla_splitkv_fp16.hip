@@ -63,6 +63,7 @@ struct F16Tile {
     static constexpr int kOWave0 = 4;                   // O waves are 4..7
     static constexpr int kNHS = HT / 16;                // 16-head sub-tiles per tile
     static constexpr int kSlot = kBT * kDK;             // halves per slot (36 KB)
+    static constexpr int kRope = kBT * kDV;             // halves: rope area of a slot (after the C_N rows)
     static constexpr int kUnits = kSlot * 2 / 1024;     // 1 KB load units per slot
     static constexpr int kLoadsPerWave = kUnits / 4;    // per O wave per block
     static constexpr int kPRow = kBT + 8;               // P row stride (halves)
@@ -74,20 +75,33 @@ struct F16Tile {
     static_assert(kSWaves <= kOWave0, "S waves");
 };
 
-// XOR swizzle of the 16-byte chunk index within a 1152-byte row. Bits of the
-// row (mod 16) are permuted so that 16 consecutive rows at one chunk hit 16
-// distinct chunk positions (S^T operand reads), and the 32-byte chunk pairs
-// read by the transpose loads of rows {r..r+3, r+8..r+11} land on 8 distinct
-// pairs. Chunks 64..71 (the rope columns, never read transposed) use the low
-// 3 bits only so they stay inside their 8-chunk group.
+// The O accumulators' reference max (log2 units) is moved only when a
+// block's max exceeds it by more than this; P scaled onto the reference is
+// then at most 2^8.
+constexpr float kLazyRescale = 8.0f;
+
+// Ring slot layout (32 rows: tokens of a block, or heads of Q*): the C_N
+// part of row r (chunks 0..63, 16 bytes each) at byte r * 1024, the rope
+// part (chunks 64..71) in a separate area at 32 KB + r * 128, so that a
+// global->LDS load unit (64 chunks) is exactly one C_N row or 8 rope rows.
+// Chunks are XOR-swizzled within a row:
+//  - C_N: chunk c of row r sits at c ^ row_swizzle(r). row_swizzle is a
+//    bijection on r mod 16, so the 16 rows read at one chunk by the first
+//    product land on 16 distinct 16-byte bank groups (rows are 1024 bytes,
+//    a multiple of the 256-byte bank period), and the transpose reads of
+//    rows {r..r+3, r+8..r+11} (swizzles {0,2,4,6} and {8,...,14} apart)
+//    cover 16 distinct groups too;
+//  - rope: chunk 64 + c' of row r sits at c' ^ rope_swizzle(r); rows are
+//    128 bytes, so rows r and r+1 share a bank period and the swizzle
+//    (r / 2) mod 8 separates the 8 row pairs of 16 consecutive rows.
 __device__ __forceinline__ int row_swizzle(int row)
 {
     return ((row >> 2) & 1) | ((row & 3) << 1) | (row & 8);
 }
 
-__device__ __forceinline__ int phys_chunk(int c, int swz)
+__device__ __forceinline__ int rope_swizzle(int row)
 {
-    return c < 64 ? (c ^ swz) : (c ^ (swz & 7));
+    return (row >> 1) & 7;
 }
 
 // s_waitcnt vmcnt(n) leaving the other counters unconstrained.
@@ -138,6 +152,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
     __shared__ __attribute__((aligned(16))) _Float16 s_p[2][HT * T::kPRow];
     __shared__ float s_m[2][2][HT];  // [P buffer][token half][head]: running max of the half
     __shared__ float s_l[2][HT];     // [token half][head]: running sum at the end of a piece
+    __shared__ float s_mref[HT];     // [head]: the O accumulators' reference max at the end of a piece
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -205,20 +220,23 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
     if (wave < T::kSWaves) {
         const int hg = wave >> 1;  // head group
         const int th = wave & 1;   // token half of each block
-        // Per-lane chunk offsets of the row-wise operand reads (row r with
-        // r % 16 == l16, logical chunk 4*kk + g). For kk < 16 the swizzle
-        // permutes kk within aligned groups of 4 and g within 0..3, so four
+        // Per-lane offsets (halves) of the row-wise operand reads: row r with
+        // r % 16 == l16, logical chunk 4*kk + g. For kk < 16 the swizzle
+        // permutes 4*(kk % 4) + g within aligned groups of 16 chunks, so four
         // offsets plus immediates cover them; the rope chunks 64..71 have two
-        // more.
-        const int swz_a = row_swizzle(l16);
+        // more, relative to the rope row.
         int a_off[6];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            a_off[j] = 8 * (4 * (j ^ (swz_a >> 2)) + ((g ^ swz_a) & 3));
+            a_off[j] = 8 * ((4 * j + g) ^ row_swizzle(l16));
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            a_off[4 + j] = 8 * (64 + ((4 * j + g) ^ (swz_a & 7)));
-        auto a_chunk = [&](int kk) { return kk < 16 ? a_off[kk & 3] + 128 * (kk >> 2) : a_off[kk - 12]; };
+            a_off[4 + j] = T::kRope + 8 * ((4 * j + g) ^ rope_swizzle(l16));
+        // operand of K-step kk of row r of a slot
+        auto a_at = [&](const _Float16 *slot, int r, int kk) -> half8 {
+            return kk < 16 ? *(const half8 *)(slot + r * kDV + a_off[kk & 3] + 128 * (kk >> 2))
+                           : *(const half8 *)(slot + r * (kDK - kDV) + a_off[kk - 12]);
+        };
 
         for_each_piece([&](int b, int p_lo, int p_hi) {
             const int slot_out = split + b;
@@ -230,12 +248,15 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
             // rows sit in the ring in the same swizzled layout as C rows.
             half8 qf[T::kNS][kDK / 32];
             {
-                const _Float16 *qs = s_ring + T::kPre * T::kSlot + (T::kSH * hg + l16) * kDK;
+                // head h of the tile is row h % 32 of Q* slot kPre + h / 32
 #pragma unroll
-                for (int ns = 0; ns < T::kNS; ++ns)
+                for (int ns = 0; ns < T::kNS; ++ns) {
+                    const int h = T::kSH * hg + 16 * ns + l16;
+                    const _Float16 *qs = s_ring + (T::kPre + h / 32) * T::kSlot;
 #pragma unroll
                     for (int kk = 0; kk < kDK / 32; ++kk)
-                        qf[ns][kk] = *(const half8 *)(qs + 16 * ns * kDK + a_chunk(kk));
+                        qf[ns][kk] = a_at(qs, h % 32, kk);
+                }
             }
             lds_barrier();  // B: the Q* slots are free again
             lds_barrier();  // C: block 0 has landed
@@ -250,7 +271,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                 if (t + 1 < nblk) {
                     const int blk = t + 1;
                     const int t0 = p_lo + blk * T::kBT + 16 * th;
-                    const _Float16 *crow = s_ring + (blk % T::kRing) * T::kSlot + (16 * th + l16) * kDK;
+                    const _Float16 *cslot = s_ring + (blk % T::kRing) * T::kSlot;
                     // ---- S^T tiles: tokens t0 + (0..15), heads of this wave.
                     // The 18 operand reads go out in batches of 3 K-steps,
                     // two batches ahead of the MFMAs that consume them.
@@ -266,7 +287,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                     auto load_batch = [&](int buf, int k0) {
 #pragma unroll
                         for (int k = 0; k < kB; ++k)
-                            ab[buf][k] = *(const half8 *)(crow + a_chunk(k0 + k));
+                            ab[buf][k] = a_at(cslot, 16 * th + l16, k0 + k);
                     };
                     load_batch(0, 0);
                     load_batch(1, kB);
@@ -338,10 +359,12 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
 #pragma unroll
                 for (int ns = 0; ns < T::kNS; ++ns) {
                     const int h = T::kSH * hg + 16 * ns + l16;
-                    const float m0 = s_m[0][0][h], m1 = s_m[0][1][h];
-                    const float mm = fmaxf(m0, m1);  // finite: the piece has a token
-                    const float ls = s_l[0][h] * fast_exp2(m0 - mm) + s_l[1][h] * fast_exp2(m1 - mm);
-                    m_part[(size_t)slot_out * num_heads + head0 + h] = mm;
+                    // the partial's max is the O waves' reference (finite, at
+                    // most kLazyRescale below the halves' maxima), so that m, l
+                    // and O share one scale
+                    const float mr = s_mref[h];
+                    const float ls = s_l[0][h] * fast_exp2(s_m[0][0][h] - mr) + s_l[1][h] * fast_exp2(s_m[0][1][h] - mr);
+                    m_part[(size_t)slot_out * num_heads + head0 + h] = mr;
                     l_part[(size_t)slot_out * num_heads + head0 + h] = ls;
                 }
             }
@@ -357,19 +380,26 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
         // of the slot, lane l fetching the logical chunk stored at position
         // 64u + l. Rows past `lim` re-read row `lim` (finite data, masked
         // later or never read).
-        // This wave's units are u = ow + 4k (k = 0..8); per unit, the lane's
-        // row (high half) and byte offset within the row (low half).
-        int unit_rc[T::kLoadsPerWave];
-#pragma unroll
-        for (int k = 0; k < T::kLoadsPerWave; ++k) {
-            const int pos = 64 * (ow + 4 * k) + lane;
-            const int row = pos / 72;
-            const int pc = pos - 72 * row;
-            unit_rc[k] = (row << 16) | (phys_chunk(pc, row_swizzle(row)) * 16);
-        }
+        // This wave's share of a 32-row block: units k = 0..7 are the C_N
+        // parts of rows ow + 4k (lane = stored chunk position; it fetches
+        // logical chunk lane ^ row_swizzle(row), where the swizzle of
+        // ow + 4k is 2*ow ^ (k & 1) ^ 8*(k >> 1 & 1)), unit 8 is the rope
+        // part of rows 8*ow .. 8*ow+7 (lane -> row 8*ow + lane/8, stored
+        // position lane % 8).
+        const int rope_row = 8 * ow + (lane >> 3);
+        const int rope_col = 2 * (kDV + 8 * ((lane & 7) ^ rope_swizzle(rope_row)));
+        // unit k of a block whose row 0 is at `base` into ring slot `slot`;
+        // rows past `lim` re-read row `lim` (finite data, masked later or
+        // never read)
         auto load_unit = [&](const _Float16 *base, int lim, int slot, int k) {
-            const int off = min(unit_rc[k] >> 16, lim) * (kDK * 2) + (unit_rc[k] & 0xffff);
-            global_to_lds16(base, off, s_ring + slot * T::kSlot + (ow + 4 * k) * 512);
+            _Float16 *dst = s_ring + slot * T::kSlot;
+            if (k < 8) {
+                const int row = ow + 4 * k;
+                const int col = 16 * (lane ^ (2 * ow) ^ (k & 1) ^ (8 * ((k >> 1) & 1)));
+                global_to_lds16(base, min(row, lim) * (kDK * 2) + col, dst + row * kDV);
+            } else {
+                global_to_lds16(base, min(rope_row, lim) * (kDK * 2) + rope_col, dst + T::kRope + 512 * ow);
+            }
         };
         // C_N^T operand of dims 128*ow + 16*dt .. +15 from a ring slot
         auto load_av = [&](const _Float16 *cs, int dt) -> half8 {
@@ -378,8 +408,8 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                 const int r0 = 8 * g + (l16 >> 2);
                 const int cl = 16 * ow + 2 * dt + ((l16 & 3) >> 1);
                 const int sub = 4 * (l16 & 1);
-                const half4 lo4 = lds_read_tr16(cs + r0 * kDK + 8 * phys_chunk(cl, row_swizzle(r0)) + sub);
-                const half4 hi4 = lds_read_tr16(cs + (r0 + 4) * kDK + 8 * phys_chunk(cl, row_swizzle(r0 + 4)) + sub);
+                const half4 lo4 = lds_read_tr16(cs + r0 * kDV + 8 * (cl ^ row_swizzle(r0)) + sub);
+                const half4 hi4 = lds_read_tr16(cs + (r0 + 4) * kDV + 8 * (cl ^ row_swizzle(r0 + 4)) + sub);
                 return half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
             } else {
                 half8 v;
@@ -387,7 +417,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int r = 8 * g + j;
-                    v[j] = cs[r * kDK + 8 * phys_chunk(col >> 3, row_swizzle(r)) + (col & 7)];
+                    v[j] = cs[r * kDV + 8 * ((col >> 3) ^ row_swizzle(r)) + (col & 7)];
                 }
                 return v;
             }
@@ -463,15 +493,20 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                         m1[hs] = s_m[blk & 1][1][16 * hs + l16];
                         pb[hs] = *(const half8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
                     }
+                    // The reference only moves when a max passes it by more
+                    // than kLazyRescale (P scaled onto it then stays <= 2^8,
+                    // well inside fp16), so the rescale is rare.
                     float alpha[T::kNHS];
                     bool moved = false;
 #pragma unroll
                     for (int hs = 0; hs < T::kNHS; ++hs) {
                         const float mn = fmaxf(m0[hs], m1[hs]);  // finite: token p_lo is in half 0
-                        alpha[hs] = fast_exp2(m_ref[hs] - mn);
-                        moved |= alpha[hs] != 1.0f;
-                        m_ref[hs] = mn;
-                        pb[hs] *= (_Float16)fast_exp2((g < 2 ? m0[hs] : m1[hs]) - mn);
+                        const bool up = mn > m_ref[hs] + kLazyRescale;  // always at the first block
+                        alpha[hs] = up ? fast_exp2(m_ref[hs] - mn) : 1.0f;
+                        moved |= up;
+                        if (up)
+                            m_ref[hs] = mn;
+                        pb[hs] *= (_Float16)fast_exp2((g < 2 ? m0[hs] : m1[hs]) - m_ref[hs]);
                     }
                     if (__builtin_amdgcn_ballot_w64(moved) != 0) {
 #pragma unroll
@@ -502,6 +537,12 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                 if (t < 0 || issue) MLA_WAIT_VMCNT(2 * T::kLoadsPerWave);
                 else MLA_WAIT_VMCNT(0);
                 lds_barrier();
+            }
+            if (g == 0) {
+#pragma unroll
+                for (int hs = 0; hs < T::kNHS; ++hs)
+                    if (ow == 0)
+                        s_mref[16 * hs + l16] = m_ref[hs];
             }
             lds_barrier();  // epilogue barrier of the S waves
             // ---- epilogue: the unnormalised O of this piece, tile by tile

@@ -11,8 +11,8 @@ synthetic (Q*, C) pair. Inputs are resident in HBM before timing starts;
 each step uses the next pair of a pool of distinct buffers totalling
 --flush-mb (default 1024 MB > the 256 MB MALL + 32 MB of L2), so no step
 finds its C in a cache. Timing is HIP events on the launch stream: one pair
-around all K steps (value, us/call) and one pair around each split-kernel
-launch (roofline.achieved for the dominant kernel).
+around all K steps (value, us/call) and one pair around K back-to-back
+split-kernel launches (roofline.achieved for the dominant kernel).
 
 Prints ONE JSON line. --workload picks another configuration (n65536, nh16,
 batched, fp32) for measurement runs; the default is the headline one.
@@ -54,6 +54,24 @@ def algorithmic(kind, n_h, total_tokens, batch=1):
     bytes_ = e * (batch * n_h * 576 + total_tokens * 576 + batch * n_h * 512)
     flops = 2 * n_h * total_tokens * (576 + 512)
     return bytes_, flops
+
+
+def roof_kernel_key(kind):
+    return "mla::splitkv_fp32_kernel" if kind == "fp32" else "mla::splitkv_fp16_kernel"
+
+
+def hbm_traffic(workload, kernel):
+    """HBM bytes per launch of the dominant kernel (FETCH_SIZE + WRITE_SIZE, each
+    scaled by its reading for a known-size device copy), from the committed
+    rocprofv3 --pmc summary profiles/hbm_traffic.json, or None when that file has
+    no entry for this workload."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f)["workloads"][workload][kernel]
+    except (OSError, KeyError, ValueError):
+        return None, None
+    return entry["fetch_bytes"] + entry["write_bytes"], "profiles/hbm_traffic_fetch_write.txt"
 
 
 def cpu_info():
@@ -235,19 +253,29 @@ def main():
     total_ms = start.elapsed_time(end)
     us_call = total_ms * 1000.0 / K
 
-    # (2) the dominant kernel alone: an event pair around each split-kernel
-    # launch on the launch stream (the combine runs outside the pairs)
-    ka = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
-    kb = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    # (2) the dominant kernel alone, K launches back to back between one event
+    # pair on the launch stream: the mean launch-to-launch time, which is what
+    # rocprofv3's kernel trace reports as the kernel's duration (an event pair
+    # around every single launch would add the events' own ~3.5 us each)
     torch.cuda.synchronize()
+    ka = torch.cuda.Event(enable_timing=True)
+    kb = torch.cuda.Event(enable_timing=True)
+    ka.record(stream)
     for i in range(K):
-        ka[i].record(stream)
         phase1(args.warmup + K + i)
-        kb[i].record(stream)
+    kb.record(stream)
+    torch.cuda.synchronize()
+    k_us = ka.elapsed_time(kb) * 1000.0 / K
+    # (3) for reference: an event pair around each split launch (combine outside)
+    pa = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    pb = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    for i in range(K):
+        pa[i].record(stream)
+        phase1(args.warmup + 2 * K + i)
+        pb[i].record(stream)
         phase2()
     torch.cuda.synchronize()
-    k_times = sorted(a.elapsed_time(b) * 1000.0 for a, b in zip(ka, kb))
-    k_us = statistics.mean(k_times)
+    k_pair_us = statistics.median(a.elapsed_time(b) * 1000.0 for a, b in zip(pa, pb))
 
     alg_bytes, alg_flops = algorithmic(kind, n_h, total, batch)
     achieved = alg_bytes / (k_us * 1e-6) / 1e9
@@ -261,11 +289,13 @@ def main():
     else:
         roof = {"bound": "mfma", "achieved": tflops, "peak": mfma_peak, "unit": "TFLOP/s",
                 "frac": tflops / mfma_peak}
+    traffic, traffic_src = hbm_traffic(args.workload, roof_kernel_key(kind))
     roof.update({
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": traffic_src,
         "kernel": "splitkv_fp16_kernel" if kind in ("fp16", "batched") else "splitkv_fp32_kernel",
         "kernel_us": k_us,
-        "kernel_us_median": statistics.median(k_times),
+        "kernel_us_event_pair_median": k_pair_us,
         "algorithmic_bytes": alg_bytes,
         "algorithmic_flops": alg_flops,
         "mfma_tflops": tflops,
