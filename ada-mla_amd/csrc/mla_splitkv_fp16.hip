@@ -22,8 +22,11 @@
 //        read by the LDS transpose read (ds_read_b64_tr_b16) one step ahead,
 //        between the MFMAs of the current block. Per head they take M = max
 //        of the two halves' running maxima, scale each half's P by
-//        2^(m_half - M) and the accumulator by 2^(M_old - M). They also feed
-//        the ring, with the global->LDS loads also placed between MFMAs.
+//        2^(m_half - M) and the accumulator by 2^(M_old - M).
+//      - the ring is fed (global->LDS loads) by the O waves, between their
+//        MFMAs, when the head tile is 64; for tiles of 16 or 32 heads two
+//        S waves suffice and waves 2 and 3 only feed the ring, which keeps
+//        the load-issue stalls off the O waves.
 //    P (fp16) and the halves' maxima pass from S to O waves through a
 //    double-buffered LDS area; one workgroup barrier per block.
 //  * C streams through a 4-slot LDS ring of 32-token blocks filled by
@@ -65,14 +68,20 @@ struct F16Tile {
     static constexpr int kSlot = kBT * kDK;             // halves per slot (36 KB)
     static constexpr int kRope = kBT * kDV;             // halves: rope area of a slot (after the C_N rows)
     static constexpr int kUnits = kSlot * 2 / 1024;     // 1 KB load units per slot
-    static constexpr int kLoadsPerWave = kUnits / 4;    // per O wave per block
     static constexpr int kPRow = kBT + 8;               // P row stride (halves)
     // Q* of the head tile is staged through the top ring slots at the start
     // of each piece (HT rows of 1152 bytes, swizzled like C rows).
     static constexpr int kQBlocks = (HT + kBT - 1) / kBT;
     static constexpr int kPre = kRing - kQBlocks;       // blocks issued with Q*
-    static_assert(kUnits % 4 == 0, "units per wave");
-    static_assert(kSWaves <= kOWave0, "S waves");
+    // Feeding of the ring (global -> LDS): the O waves at HT = 64, else the
+    // two waves after the S waves; each feeder owns kFeedRows rows of a block.
+    static constexpr bool kOFeeds = kSWaves == kOWave0;
+    static constexpr int kFeeders = kOFeeds ? 4 : 2;
+    static constexpr int kFeedRows = kBT / kFeeders;
+    static constexpr int kFeedUnits = kFeedRows + kFeedRows / 8;  // C_N rows + rope units
+    static_assert(kFeeders * kFeedUnits == kUnits, "feeder split");
+    static_assert(kOFeeds || kSWaves == 2, "feeder waves are 2 and 3");
+    static_assert(3 * kFeedUnits <= 63, "vmcnt range");
 };
 
 // The O accumulators' reference max (log2 units) is moved only when a
@@ -369,197 +378,236 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                 }
             }
         });
-    } else if (wave >= T::kOWave0) {
-        const int ow = wave - T::kOWave0;  // column quarter
-        // The O waves issue first when both waves of a SIMD are ready: their
-        // P reads at the start of a step then reach the LDS ahead of the S
-        // waves' operand reads, and their MFMAs carry the step.
-        __builtin_amdgcn_s_setprio(2);
-        // Global -> LDS load of unit u (1 KB) of a 32-row block whose row 0
-        // is at `base` into ring slot `slot`: chunk positions [64u, 64u + 64)
-        // of the slot, lane l fetching the logical chunk stored at position
-        // 64u + l. Rows past `lim` re-read row `lim` (finite data, masked
-        // later or never read).
-        // This wave's share of a 32-row block: units k = 0..7 are the C_N
-        // parts of rows ow + 4k (lane = stored chunk position; it fetches
-        // logical chunk lane ^ row_swizzle(row), where the swizzle of
-        // ow + 4k is 2*ow ^ (k & 1) ^ 8*(k >> 1 & 1)), unit 8 is the rope
-        // part of rows 8*ow .. 8*ow+7 (lane -> row 8*ow + lane/8, stored
-        // position lane % 8).
-        const int rope_row = 8 * ow + (lane >> 3);
-        const int rope_col = 2 * (kDV + 8 * ((lane & 7) ^ rope_swizzle(rope_row)));
-        // unit k of a block whose row 0 is at `base` into ring slot `slot`;
-        // rows past `lim` re-read row `lim` (finite data, masked later or
-        // never read)
+    } else {
+        // ---- global -> LDS feeding of the ring. kFeeders waves share each
+        // block: feeder d owns rows [kFeedRows*d, +kFeedRows): one load unit
+        // (1 KB) per row for the C_N part (lane = stored chunk position; it
+        // fetches logical chunk lane ^ row_swizzle(row)) and one per 8 rows
+        // for the rope part (lane -> row 8*ru + lane/8, stored position
+        // lane % 8). The O waves feed at HT = 64; otherwise waves 2 and 3,
+        // which have no other role, do.
+        const int feeder = T::kOFeeds ? wave - T::kOWave0 : wave - T::kSWaves;
+        // unit k of a 32-row block whose row 0 is at `base` into ring slot
+        // `slot`; rows past `lim` re-read row `lim` (finite data, masked
+        // later or never read)
         auto load_unit = [&](const _Float16 *base, int lim, int slot, int k) {
             _Float16 *dst = s_ring + slot * T::kSlot;
-            if (k < 8) {
-                const int row = ow + 4 * k;
-                const int col = 16 * (lane ^ (2 * ow) ^ (k & 1) ^ (8 * ((k >> 1) & 1)));
+            if (k < T::kFeedRows) {
+                const int row = T::kFeedRows * feeder + k;
+                const int col = 16 * (lane ^ row_swizzle(row));
                 global_to_lds16(base, min(row, lim) * (kDK * 2) + col, dst + row * kDV);
             } else {
-                global_to_lds16(base, min(rope_row, lim) * (kDK * 2) + rope_col, dst + T::kRope + 512 * ow);
+                const int ru = (T::kFeedRows / 8) * feeder + (k - T::kFeedRows);
+                const int rrow = 8 * ru + (lane >> 3);
+                const int rcol = 2 * (kDV + 8 * ((lane & 7) ^ rope_swizzle(rrow)));
+                global_to_lds16(base, min(rrow, lim) * (kDK * 2) + rcol, dst + T::kRope + 512 * ru);
             }
         };
-        // C_N^T operand of dims 128*ow + 16*dt .. +15 from a ring slot
-        auto load_av = [&](const _Float16 *cs, int dt) -> half8 {
-            if constexpr (kTr) {
-                // lane (g, j): rows 8g + j/4 (+4), dims 128*ow + 16*dt + 4*(j%4) .. +3
-                const int r0 = 8 * g + (l16 >> 2);
-                const int cl = 16 * ow + 2 * dt + ((l16 & 3) >> 1);
-                const int sub = 4 * (l16 & 1);
-                const half4 lo4 = lds_read_tr16(cs + r0 * kDV + 8 * (cl ^ row_swizzle(r0)) + sub);
-                const half4 hi4 = lds_read_tr16(cs + (r0 + 4) * kDV + 8 * (cl ^ row_swizzle(r0 + 4)) + sub);
-                return half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-            } else {
-                half8 v;
-                const int col = 128 * ow + 16 * dt + l16;
+        // Prologue of a piece: Q* of the head tile into the top kQBlocks
+        // slots first (the S waves need it before any block), then blocks
+        // 0..kPre-1; after the S waves hold Q* in registers (barrier B), the
+        // remaining blocks up to 3. Blocks past the last re-read the last
+        // token, so the wait counts are constants.
+        auto feed_prologue = [&](int b, int p_lo, int p_hi, auto &&issue_unit) {
+            const _Float16 *qb = q + ((size_t)b * num_heads + head0) * kDK;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int r = 8 * g + j;
-                    v[j] = cs[r * kDV + 8 * ((col >> 3) ^ row_swizzle(r)) + (col & 7)];
-                }
-                return v;
-            }
-        };
-
-        for_each_piece([&](int b, int p_lo, int p_hi) {
-            const int slot_out = split + b;
-            const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
-            // unit k (0..8) of this wave's share of block blk; a block past
-            // the last re-reads the last token only
-            auto issue_unit = [&](int blk, int k) {
-                const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
-                load_unit(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk % T::kRing, k);
-            };
-            lds_barrier();  // piece start
-            // Prologue: Q* of the head tile into the top kQBlocks slots first
-            // (the S waves need it before any block), then blocks 0..kPre-1.
-            {
-                const _Float16 *qb = q + ((size_t)b * num_heads + head0) * kDK;
+            for (int j = 0; j < T::kQBlocks; ++j)
 #pragma unroll
-                for (int j = 0; j < T::kQBlocks; ++j)
-#pragma unroll
-                    for (int k = 0; k < T::kLoadsPerWave; ++k)
-                        load_unit(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, k);
-            }
+                for (int k = 0; k < T::kFeedUnits; ++k)
+                    load_unit(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, k);
 #pragma unroll
             for (int blk = 0; blk < T::kPre; ++blk)
 #pragma unroll
-                for (int k = 0; k < T::kLoadsPerWave; ++k)
+                for (int k = 0; k < T::kFeedUnits; ++k)
                     issue_unit(blk, k);
-            MLA_WAIT_VMCNT(T::kPre * T::kLoadsPerWave);  // Q* has landed
+            MLA_WAIT_VMCNT(T::kPre * T::kFeedUnits);  // Q* has landed
             lds_barrier();  // A
             lds_barrier();  // B: the S waves hold Q* in registers
 #pragma unroll
             for (int blk = T::kPre; blk < T::kRing; ++blk)
 #pragma unroll
-                for (int k = 0; k < T::kLoadsPerWave; ++k)
+                for (int k = 0; k < T::kFeedUnits; ++k)
                     issue_unit(blk, k);
-            MLA_WAIT_VMCNT((T::kRing - 1) * T::kLoadsPerWave);  // block 0 has landed
+            MLA_WAIT_VMCNT((T::kRing - 1) * T::kFeedUnits);  // block 0 has landed
             lds_barrier();  // C
+        };
+        // End of step t: block t+2 (the S waves' next) must have landed;
+        // blocks t+3 and t+4 may stay in flight.
+        auto feed_wait = [&](bool issued, int t) {
+            if (t < 0 || issued) MLA_WAIT_VMCNT(2 * T::kFeedUnits);
+            else MLA_WAIT_VMCNT(0);
+        };
 
-            floatx4 o[T::kNHS][8];
-            float m_ref[T::kNHS];  // per head l16 of sub-tile hs: the accumulator's reference max
+        if (wave >= T::kOWave0) {
+            const int ow = wave - T::kOWave0;  // column quarter
+            // When the O waves also feed the ring (HT = 64) they carry the
+            // step: they issue first when both waves of a SIMD are ready, so
+            // their P reads reach the LDS ahead of the S waves' operand reads.
+            // With dedicated feeders the S waves carry the step and equal
+            // priorities are best.
+            if constexpr (T::kOFeeds)
+                __builtin_amdgcn_s_setprio(2);
+            // C_N^T operand of dims 128*ow + 16*dt .. +15 from a ring slot
+            auto load_av = [&](const _Float16 *cs, int dt) -> half8 {
+                if constexpr (kTr) {
+                    // lane (g, j): rows 8g + j/4 (+4), dims 128*ow + 16*dt + 4*(j%4) .. +3
+                    const int r0 = 8 * g + (l16 >> 2);
+                    const int cl = 16 * ow + 2 * dt + ((l16 & 3) >> 1);
+                    const int sub = 4 * (l16 & 1);
+                    const half4 lo4 = lds_read_tr16(cs + r0 * kDV + 8 * (cl ^ row_swizzle(r0)) + sub);
+                    const half4 hi4 = lds_read_tr16(cs + (r0 + 4) * kDV + 8 * (cl ^ row_swizzle(r0 + 4)) + sub);
+                    return half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                } else {
+                    half8 v;
+                    const int col = 128 * ow + 16 * dt + l16;
 #pragma unroll
-            for (int hs = 0; hs < T::kNHS; ++hs) {
-                m_ref[hs] = -INFINITY;
+                    for (int j = 0; j < 8; ++j) {
+                        const int r = 8 * g + j;
+                        v[j] = cs[r * kDV + 8 * ((col >> 3) ^ row_swizzle(r)) + (col & 7)];
+                    }
+                    return v;
+                }
+            };
+
+            for_each_piece([&](int b, int p_lo, int p_hi) {
+                const int slot_out = split + b;
+                const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
+                // unit k of this wave's share of block blk; a block past the
+                // last re-reads the last token only
+                auto issue_unit = [&](int blk, int k) {
+                    const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
+                    load_unit(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk % T::kRing, k);
+                };
+                lds_barrier();  // piece start
+                if constexpr (T::kOFeeds) {
+                    feed_prologue(b, p_lo, p_hi, issue_unit);
+                } else {
+                    lds_barrier();  // A
+                    lds_barrier();  // B
+                    lds_barrier();  // C
+                }
+
+                floatx4 o[T::kNHS][8];
+                float m_ref[T::kNHS];  // per head l16 of sub-tile hs: the accumulator's reference max
+#pragma unroll
+                for (int hs = 0; hs < T::kNHS; ++hs) {
+                    m_ref[hs] = -INFINITY;
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt)
+                        o[hs][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+                // C_N^T fragments of the block the next step accumulates; each
+                // step reloads them for its successor right after the MFMAs
+                // that consume them
+                half8 av[8];
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt)
-                    o[hs][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-            }
-            // C_N^T fragments of the block the next step accumulates; each
-            // step reloads them for its successor right after the MFMAs that
-            // consume them
-            half8 av[8];
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt)
-                av[dt] = load_av(s_ring, dt);
+                    av[dt] = load_av(s_ring, dt);
 
-            for (int t = -1; t < nblk; ++t) {
-                // block t+4 goes into the slot of block t, which every wave
-                // has finished reading (its C_N^T fragments are in av)
-                const bool issue = t >= 0 && t + T::kRing < nblk;
-                if (t >= 0) {
-                    const int blk = t;
-                    // ---- common reference max of the two token halves; P of
-                    // the half this lane feeds (tokens 8g..8g+7: half g/2) is
-                    // scaled onto it, the accumulator moves by 2^(M_old - M)
-                    half8 pb[T::kNHS];
-                    float m0[T::kNHS], m1[T::kNHS];
+                for (int t = -1; t < nblk; ++t) {
+                    // block t+4 goes into the slot of block t, which every
+                    // wave has finished reading (its C_N^T fragments are in av)
+                    const bool issue = T::kOFeeds && t >= 0 && t + T::kRing < nblk;
+                    if (t >= 0) {
+                        const int blk = t;
+                        // ---- common reference max of the two token halves; P
+                        // of the half this lane feeds (tokens 8g..8g+7: half
+                        // g/2) is scaled onto it, the accumulator moves by
+                        // 2^(M_old - M)
+                        half8 pb[T::kNHS];
+                        float m0[T::kNHS], m1[T::kNHS];
 #pragma unroll
-                    for (int hs = 0; hs < T::kNHS; ++hs) {
-                        m0[hs] = s_m[blk & 1][0][16 * hs + l16];
-                        m1[hs] = s_m[blk & 1][1][16 * hs + l16];
-                        pb[hs] = *(const half8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
+                        for (int hs = 0; hs < T::kNHS; ++hs) {
+                            m0[hs] = s_m[blk & 1][0][16 * hs + l16];
+                            m1[hs] = s_m[blk & 1][1][16 * hs + l16];
+                            pb[hs] = *(const half8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
+                        }
+                        // The reference only moves when a max passes it by more
+                        // than kLazyRescale (P scaled onto it then stays <= 2^8,
+                        // well inside fp16), so the rescale is rare.
+                        float alpha[T::kNHS];
+                        bool moved = false;
+#pragma unroll
+                        for (int hs = 0; hs < T::kNHS; ++hs) {
+                            const float mn = fmaxf(m0[hs], m1[hs]);  // finite: token p_lo is in half 0
+                            const bool up = mn > m_ref[hs] + kLazyRescale;  // always at the first block
+                            alpha[hs] = up ? fast_exp2(m_ref[hs] - mn) : 1.0f;
+                            moved |= up;
+                            if (up)
+                                m_ref[hs] = mn;
+                            pb[hs] *= (_Float16)fast_exp2((g < 2 ? m0[hs] : m1[hs]) - m_ref[hs]);
+                        }
+                        if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+#pragma unroll
+                            for (int hs = 0; hs < T::kNHS; ++hs)
+#pragma unroll
+                                for (int dt = 0; dt < 8; ++dt)
+                                    o[hs][dt] *= alpha[hs];
+                        }
+                        // ---- O^T[dims 128*ow .. +128][heads] += C_N^T P^T, with
+                        // the next block's operand reads (and, when the O
+                        // waves feed, this step's global->LDS loads) placed
+                        // between the MFMAs
+                        const _Float16 *cn = s_ring + ((blk + 1) % T::kRing) * T::kSlot;
+#pragma unroll
+                        for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+                            for (int hs = 0; hs < T::kNHS; ++hs)
+                                o[hs][dt] = mfma16x16x32(av[dt], pb[hs], o[hs][dt]);
+                            av[dt] = load_av(cn, dt);
+                            if (issue)
+                                issue_unit(blk + T::kRing, dt);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                        if (issue) {
+#pragma unroll
+                            for (int k = 8; k < T::kFeedUnits; ++k)
+                                issue_unit(blk + T::kRing, k);
+                        }
                     }
-                    // The reference only moves when a max passes it by more
-                    // than kLazyRescale (P scaled onto it then stays <= 2^8,
-                    // well inside fp16), so the rescale is rare.
-                    float alpha[T::kNHS];
-                    bool moved = false;
-#pragma unroll
-                    for (int hs = 0; hs < T::kNHS; ++hs) {
-                        const float mn = fmaxf(m0[hs], m1[hs]);  // finite: token p_lo is in half 0
-                        const bool up = mn > m_ref[hs] + kLazyRescale;  // always at the first block
-                        alpha[hs] = up ? fast_exp2(m_ref[hs] - mn) : 1.0f;
-                        moved |= up;
-                        if (up)
-                            m_ref[hs] = mn;
-                        pb[hs] *= (_Float16)fast_exp2((g < 2 ? m0[hs] : m1[hs]) - m_ref[hs]);
-                    }
-                    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
-#pragma unroll
-                        for (int hs = 0; hs < T::kNHS; ++hs)
-#pragma unroll
-                            for (int dt = 0; dt < 8; ++dt)
-                                o[hs][dt] *= alpha[hs];
-                    }
-                    // ---- O^T[dims 128*ow .. +128][heads] += C_N^T P^T, with the
-                    // next block's operand reads and this step's global->LDS
-                    // loads placed between the MFMAs
-                    const _Float16 *cn = s_ring + ((blk + 1) % T::kRing) * T::kSlot;
-#pragma unroll
-                    for (int dt = 0; dt < 8; ++dt) {
-#pragma unroll
-                        for (int hs = 0; hs < T::kNHS; ++hs)
-                            o[hs][dt] = mfma16x16x32(av[dt], pb[hs], o[hs][dt]);
-                        av[dt] = load_av(cn, dt);
-                        if (issue)
-                            issue_unit(blk + T::kRing, dt);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                    if (issue)
-                        issue_unit(blk + T::kRing, 8);
+                    if constexpr (T::kOFeeds)
+                        feed_wait(issue, t);
+                    lds_barrier();
                 }
-                // ---- block t+2 (the S waves' next) must have landed before
-                // the barrier; blocks t+3 and t+4 may stay in flight
-                if (t < 0 || issue) MLA_WAIT_VMCNT(2 * T::kLoadsPerWave);
-                else MLA_WAIT_VMCNT(0);
-                lds_barrier();
-            }
-            if (g == 0) {
+                if (g == 0) {
+#pragma unroll
+                    for (int hs = 0; hs < T::kNHS; ++hs)
+                        if (ow == 0)
+                            s_mref[16 * hs + l16] = m_ref[hs];
+                }
+                lds_barrier();  // epilogue barrier of the S waves
+                // ---- epilogue: the unnormalised O of this piece, tile by tile
+                float *obase = o_part + (size_t)slot_out * num_heads * kDV + lane * 4;
 #pragma unroll
                 for (int hs = 0; hs < T::kNHS; ++hs)
-                    if (ow == 0)
-                        s_mref[16 * hs + l16] = m_ref[hs];
-            }
-            lds_barrier();  // epilogue barrier of the S waves
-            // ---- epilogue: the unnormalised O of this piece, tile by tile
-            float *obase = o_part + (size_t)slot_out * num_heads * kDV + lane * 4;
 #pragma unroll
-            for (int hs = 0; hs < T::kNHS; ++hs)
+                    for (int dt = 0; dt < 8; ++dt)
+                        *(floatx4 *)(obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt)) = o[hs][dt];
+            });
+        } else {
+            // dedicated feeder waves (head tiles of 16 or 32 heads)
+            for_each_piece([&](int b, int p_lo, int p_hi) {
+                const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
+                auto issue_unit = [&](int blk, int k) {
+                    const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
+                    load_unit(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk % T::kRing, k);
+                };
+                lds_barrier();  // piece start
+                feed_prologue(b, p_lo, p_hi, issue_unit);
+                for (int t = -1; t < nblk; ++t) {
+                    // block t+4 into the slot of block t
+                    const bool issue = t >= 0 && t + T::kRing < nblk;
+                    if (issue) {
 #pragma unroll
-                for (int dt = 0; dt < 8; ++dt)
-                    *(floatx4 *)(obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt)) = o[hs][dt];
-        });
-    } else {
-        // waves with no role at this head-tile size keep the barrier count
-        for_each_piece([&](int, int p_lo, int p_hi) {
-            const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
-            for (int i = 0; i < nblk + 6; ++i)
-                lds_barrier();
-        });
+                        for (int k = 0; k < T::kFeedUnits; ++k)
+                            issue_unit(t + T::kRing, k);
+                    }
+                    feed_wait(issue, t);
+                    lds_barrier();
+                }
+                lds_barrier();  // epilogue barrier of the S waves
+            });
+        }
     }
 }
 
