@@ -62,7 +62,7 @@ struct F16Tile {
     static constexpr int kNS = kSH / 16;                // 16-head sub-tiles per S wave
     static constexpr int kNHG = HT / kSH;               // head groups
     static constexpr int kSWaves = 2 * kNHG;            // S waves: (head group, token half)
-    static constexpr int kChains = 8 / kNS;             // accumulation chains per sub-tile
+    static constexpr int kChains = 4 / kNS;             // accumulation chains per sub-tile
     static constexpr int kOWave0 = 4;                   // O waves are 4..7
     static constexpr int kNHS = HT / 16;                // 16-head sub-tiles per tile
     static constexpr int kSlot = kBT * kDK;             // halves per slot (36 KB)
@@ -204,7 +204,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
     }
     // Calls body(b, p_lo, p_hi) for every non-empty piece [p_lo, p_hi) of
     // sequence b inside this chunk. Every wave walks the same pieces and,
-    // per piece, passes the same number of barriers (nblk + 6).
+    // per piece, passes the same number of barriers (nblk + 5).
     auto for_each_piece = [&](auto &&body) {
         for (int b = b_first; b < nseq; ++b) {
             int seq_lo = 0, seq_hi = total_tokens;
@@ -219,6 +219,56 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
             if (p_lo < p_hi)
                 body(b, p_lo, p_hi);
         }
+    };
+
+    // ---- global -> LDS loads of the ring (one 1 KB load unit per call):
+    // the C_N part of row `row` of a 32-row block whose row 0 is at `base`
+    // (lane = stored chunk position; it fetches logical chunk
+    // lane ^ row_swizzle(row)), or the rope part of rows 8*ru .. 8*ru+7
+    // (lane -> row 8*ru + lane/8, stored position lane % 8). Rows past `lim`
+    // re-read row `lim` (finite data, masked later or never read).
+    // The lane index is passed through an empty asm so that the offsets are
+    // recomputed at each load (a few VALU ops) instead of being kept live,
+    // or spilled, across the piece: a spill reload here would make the
+    // compiler wait for every outstanding global->LDS load.
+    auto dma_row = [&](const _Float16 *base, int lim, int slot, int row) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        global_to_lds16(base, min(row, lim) * (kDK * 2) + 16 * (ln ^ row_swizzle(row)),
+                        s_ring + slot * T::kSlot + row * kDV);
+    };
+    auto dma_rope = [&](const _Float16 *base, int lim, int slot, int ru) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int rrow = 8 * ru + (ln >> 3);
+        global_to_lds16(base, min(rrow, lim) * (kDK * 2) + 2 * (kDV + 8 * ((ln & 7) ^ rope_swizzle(rrow))),
+                        s_ring + slot * T::kSlot + T::kRope + 512 * ru);
+    };
+    // Prologue loads of a piece, issued by all 8 waves (wave w: C_N rows
+    // 4w..4w+3 and, for w < 4, the rope rows 8w..8w+7 of each block): Q* of
+    // the head tile into the top kQBlocks slots first, then blocks
+    // 0..kPre-1. Each wave waits for its own loads; the barrier after this
+    // (A) then publishes Q* and those blocks to every wave.
+    auto prologue_loads = [&](int b, int p_lo, int p_hi) {
+        const _Float16 *qb = q + ((size_t)b * num_heads + head0) * kDK;
+#pragma unroll
+        for (int j = 0; j < T::kQBlocks; ++j) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                dma_row(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, 4 * wave + r);
+            if (wave < 4)
+                dma_rope(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, wave);
+        }
+#pragma unroll
+        for (int blk = 0; blk < T::kPre; ++blk) {
+            const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                dma_row(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk, 4 * wave + r);
+            if (wave < 4)
+                dma_rope(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk, wave);
+        }
+        MLA_WAIT_VMCNT(0);
     };
 
     // Each role runs its own piece loop and step loop (t = -1 .. nblk-1: S
@@ -251,7 +301,8 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
             const int slot_out = split + b;
             const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
             lds_barrier();  // piece start: buffers are reused from the previous piece
-            lds_barrier();  // A: Q* has landed in the top ring slots
+            prologue_loads(b, p_lo, p_hi);
+            lds_barrier();  // A: Q* and blocks 0..kPre-1 have landed
             // Q* fragments (B operand of S^T = C Q*^T): lane holds head
             // kSH*hg + 16*ns + l16 of the tile, dims 32*kk + 8*g .. +7. Q*
             // rows sit in the ring in the same swizzled layout as C rows.
@@ -268,7 +319,6 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                 }
             }
             lds_barrier();  // B: the Q* slots are free again
-            lds_barrier();  // C: block 0 has landed
 
             float m_run[T::kNS], l_lane[T::kNS];  // running max (uniform over g); per-lane partial sum
 #pragma unroll
@@ -387,49 +437,22 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
         // lane % 8). The O waves feed at HT = 64; otherwise waves 2 and 3,
         // which have no other role, do.
         const int feeder = T::kOFeeds ? wave - T::kOWave0 : wave - T::kSWaves;
-        // unit k of a 32-row block whose row 0 is at `base` into ring slot
-        // `slot`; rows past `lim` re-read row `lim` (finite data, masked
-        // later or never read)
+        // unit k (0..kFeedUnits-1) of this feeder's share of a block: C_N
+        // row kFeedRows*feeder + k, or a rope unit of those rows
         auto load_unit = [&](const _Float16 *base, int lim, int slot, int k) {
-            _Float16 *dst = s_ring + slot * T::kSlot;
-            if (k < T::kFeedRows) {
-                const int row = T::kFeedRows * feeder + k;
-                const int col = 16 * (lane ^ row_swizzle(row));
-                global_to_lds16(base, min(row, lim) * (kDK * 2) + col, dst + row * kDV);
-            } else {
-                const int ru = (T::kFeedRows / 8) * feeder + (k - T::kFeedRows);
-                const int rrow = 8 * ru + (lane >> 3);
-                const int rcol = 2 * (kDV + 8 * ((lane & 7) ^ rope_swizzle(rrow)));
-                global_to_lds16(base, min(rrow, lim) * (kDK * 2) + rcol, dst + T::kRope + 512 * ru);
-            }
+            if (k < T::kFeedRows)
+                dma_row(base, lim, slot, T::kFeedRows * feeder + k);
+            else
+                dma_rope(base, lim, slot, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
         };
-        // Prologue of a piece: Q* of the head tile into the top kQBlocks
-        // slots first (the S waves need it before any block), then blocks
-        // 0..kPre-1; after the S waves hold Q* in registers (barrier B), the
-        // remaining blocks up to 3. Blocks past the last re-read the last
-        // token, so the wait counts are constants.
-        auto feed_prologue = [&](int b, int p_lo, int p_hi, auto &&issue_unit) {
-            const _Float16 *qb = q + ((size_t)b * num_heads + head0) * kDK;
-#pragma unroll
-            for (int j = 0; j < T::kQBlocks; ++j)
-#pragma unroll
-                for (int k = 0; k < T::kFeedUnits; ++k)
-                    load_unit(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, k);
-#pragma unroll
-            for (int blk = 0; blk < T::kPre; ++blk)
-#pragma unroll
-                for (int k = 0; k < T::kFeedUnits; ++k)
-                    issue_unit(blk, k);
-            MLA_WAIT_VMCNT(T::kPre * T::kFeedUnits);  // Q* has landed
-            lds_barrier();  // A
-            lds_barrier();  // B: the S waves hold Q* in registers
+        // After barrier B (the S waves hold Q* in registers) the feeders load
+        // blocks kPre..3 into the slots Q* used.
+        auto feed_rest = [&](auto &&issue_unit) {
 #pragma unroll
             for (int blk = T::kPre; blk < T::kRing; ++blk)
 #pragma unroll
                 for (int k = 0; k < T::kFeedUnits; ++k)
                     issue_unit(blk, k);
-            MLA_WAIT_VMCNT((T::kRing - 1) * T::kFeedUnits);  // block 0 has landed
-            lds_barrier();  // C
         };
         // End of step t: block t+2 (the S waves' next) must have landed;
         // blocks t+3 and t+4 may stay in flight.
@@ -479,13 +502,11 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                     load_unit(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk % T::kRing, k);
                 };
                 lds_barrier();  // piece start
-                if constexpr (T::kOFeeds) {
-                    feed_prologue(b, p_lo, p_hi, issue_unit);
-                } else {
-                    lds_barrier();  // A
-                    lds_barrier();  // B
-                    lds_barrier();  // C
-                }
+                prologue_loads(b, p_lo, p_hi);
+                lds_barrier();  // A
+                lds_barrier();  // B
+                if constexpr (T::kOFeeds)
+                    feed_rest(issue_unit);
 
                 floatx4 o[T::kNHS][8];
                 float m_ref[T::kNHS];  // per head l16 of sub-tile hs: the accumulator's reference max
@@ -593,7 +614,10 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                     load_unit(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk % T::kRing, k);
                 };
                 lds_barrier();  // piece start
-                feed_prologue(b, p_lo, p_hi, issue_unit);
+                prologue_loads(b, p_lo, p_hi);
+                lds_barrier();  // A
+                lds_barrier();  // B
+                feed_rest(issue_unit);
                 for (int t = -1; t < nblk; ++t) {
                     // block t+4 into the slot of block t
                     const bool issue = t >= 0 && t + T::kRing < nblk;
