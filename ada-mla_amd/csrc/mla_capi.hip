@@ -86,7 +86,7 @@ double modelled_us(const Plan &p, int num_heads, int batch, int cu_count)
     const double rounds = std::ceil((double)wgs / cu_count);
     const double steps = std::ceil((double)p.chunk / p.block_tokens) + 1.0;
     const double share = (p.n_head_tiles > 1 && !p.xcd_remap) ? 1.3 : 1.0;
-    const double partial_bytes = (double)p.n_slots * num_heads * (kDV + 2) * 4.0;
+    const double partial_bytes = (double)p.n_slots * num_heads * (kDV * p.part_bytes + 8);
     // the combine merges up to 128 slots of a tile per memory round trip
     const double slots_per_seq = std::ceil((double)p.n_slots / batch);
     const double combine_trips = std::ceil(slots_per_seq / 128.0);
@@ -107,6 +107,7 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
         p.n_chunks = 0;
         p.n_slots = batch;  // unused; keeps the workspace non-empty
         p.xcd_remap = 0;
+        p.part_bytes = fp32 ? 4 : 2;
         return p;
     }
     if (fp32) {
@@ -117,6 +118,7 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
         if (w <= 0)
             w = std::min(cu_count / p.n_head_tiles, ceil_div(total_tokens, kMinSplitTokensF32));
         set_chunks(p, total_tokens, batch, w);
+        p.part_bytes = 4;
         return p;
     }
     // fp16: the head tile (64, 32 or 16 heads per workgroup) and the split
@@ -132,6 +134,7 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
         c.head_tile = ht;
         c.block_tokens = 32;
         c.n_head_tiles = num_heads / ht;
+        c.part_bytes = 2;
         int w_lo = 1, w_hi = std::max(1, std::min(cu_count / c.n_head_tiles, ceil_div(total_tokens, c.block_tokens)));
         if (num_splits > 0)
             w_lo = w_hi = num_splits;
@@ -150,7 +153,7 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
 size_t partials_bytes(const Plan &p, int num_heads)
 {
     const size_t rows = (size_t)p.n_slots * (size_t)num_heads;
-    return align_up(rows * kDV * sizeof(float)) + 2 * align_up(rows * sizeof(float));
+    return align_up(rows * kDV * (size_t)p.part_bytes) + 2 * align_up(rows * sizeof(float));
 }
 
 Partials carve_partials(void *ws, const Plan &p, int num_heads)
@@ -158,8 +161,8 @@ Partials carve_partials(void *ws, const Plan &p, int num_heads)
     const size_t rows = (size_t)p.n_slots * (size_t)num_heads;
     char *base = static_cast<char *>(ws);
     Partials w;
-    w.o = reinterpret_cast<float *>(base);
-    base += align_up(rows * kDV * sizeof(float));
+    w.o = base;
+    base += align_up(rows * kDV * (size_t)p.part_bytes);
     w.m = reinterpret_cast<float *>(base);
     base += align_up(rows * sizeof(float));
     w.l = reinterpret_cast<float *>(base);

@@ -1,88 +1,110 @@
 // LSE-weighted merge of split-KV partials into the decode output:
-//   m = max_s m_s,  l = sum_s l_s 2^(m_s - m),  O* = sum_s O_s 2^(m_s - m) / l
-// over the slots s of one (sequence, head); m_s are in log2 units.
+//   m = max_s m_s,  l = sum_s l_s 2^(m_s - m),  O* = sum_s w_s O_s / l
+// over the slots s of one (sequence, head); m_s are in log2 units, and
+// w_s = l_s 2^(m_s - m) for partials normalised by their sum (fp16 path) or
+// 2^(m_s - m) for unnormalised ones (fp32 path).
 //
 // Replaces mla_decode_combine (reference csrc/mla_decode_splitk_fwd.cuh:894-939),
 // which ran one 128-thread block per head looping serially over the splits
 // with the weight e^(m_s - m) recomputed per column. Here:
-//  * fp32 partials; the max starts at -inf; an empty sequence writes zeros;
+//  * the max starts at -inf; an empty sequence writes zeros;
 //  * a sequence's slot range follows from the split plan (any number of
 //    splits, any batch);
-//  * one 512-thread workgroup per (16 x 16 output tile, sequence). The
+//  * the unit of work is an item = (16 x 16 output tile, sequence). The
 //    partial O is stored tile by tile in MFMA accumulator order
-//    (frag_offset), so a wave reads one slot's tile as 1 KB of contiguous
-//    memory; lane (g, h) owns head h, dims 4g..4g+3 of the tile. Each of the
-//    8 waves merges every 8th slot online (running max, rescaled sums) with
-//    the loads of the next 8 slots in flight while it merges the current 8
-//    (128 slots per memory round trip), and the 8 wave results are merged
-//    through LDS.
+//    (frag_offset), so a wave reads one slot's tile as one contiguous run
+//    (512 B in fp16, 1 KB in fp32); lane (g, h) owns head h, dims 4g..4g+3.
+//  * W waves share an item (W = 1..16, chosen from the slots per sequence so
+//    that a wave merges about 4 slots): wave k merges slots k, k + W, ...
+//    online (running max, rescaled sums), with the loads of its next 8 slots
+//    in flight while it merges the current 8, and the W wave results are
+//    merged through LDS. A workgroup holds max(8, W) waves, i.e. 8 / W items
+//    for W < 8.
+#include <type_traits>
+
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
 
 namespace mla {
 namespace {
 
-constexpr int kWaves = 8;
 constexpr int kU = 8;  // slots per load batch and wave
 
+template <typename PartT>
 struct SlotBatch {
-    floatx4 v[kU];
+    using V = typename std::conditional<sizeof(PartT) == 2, half4, floatx4>::type;
+    V v[kU];
     float m[kU];
     float l[kU];
 };
 
-template <bool kOutF32>
-__global__ __launch_bounds__(64 * kWaves)
-void combine_kernel(const float *__restrict__ o_part,
+__device__ __forceinline__ floatx4 to_f32(const floatx4 &v) { return v; }
+__device__ __forceinline__ floatx4 to_f32(const half4 &v)
+{
+    return floatx4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+
+template <typename PartT, int W, bool kOutF32>
+__global__ __launch_bounds__(64 * (W > 8 ? W : 8))
+void combine_kernel(const PartT *__restrict__ o_part,
                     const float *__restrict__ m_part,
                     const float *__restrict__ l_part,
                     const int *__restrict__ cu_seqlens,
                     void *__restrict__ out,
-                    int num_heads, int total_tokens, int chunk)
+                    int num_heads, int total_tokens, int chunk, int n_items)
 {
-    __shared__ float s_m[kWaves][64];
-    __shared__ float s_l[kWaves][64];
-    __shared__ floatx4 s_o[kWaves][64];
+    constexpr int kWaves = W > 8 ? W : 8;
+    constexpr int kItems = kWaves / W;
+    constexpr bool kNorm = sizeof(PartT) == 2;  // fp16 partials are normalised by l
+    using Batch = SlotBatch<PartT>;
+    using V = typename Batch::V;
+    __shared__ float s_m[W > 1 ? kWaves : 1][64];
+    __shared__ float s_l[W > 1 ? kWaves : 1][64];
+    __shared__ floatx4 s_o[W > 1 ? kWaves : 1][64];
 
-    const int tile = blockIdx.x;  // (head / 16) * 32 + dim / 16
-    const int b = blockIdx.y;
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
+    const int item = blockIdx.x * kItems + w / W;
+    const int k = w % W;  // this wave's place among the item's W waves
+    const int n_tiles = num_heads / 16 * (kDV / 16);
+    const bool valid = item < n_items;
+    const int tile = valid ? item % n_tiles : 0;  // (head / 16) * 32 + dim / 16
+    const int b = valid ? item / n_tiles : 0;
     const int head = (tile >> 5) * 16 + (lane & 15);
     const int dim0 = (tile & 31) * 16 + 4 * (lane >> 4);
 
-    int lo = 0, hi = total_tokens;
-    if (cu_seqlens) {
+    int lo = 0, hi = valid ? total_tokens : 0;
+    if (valid && cu_seqlens) {
         lo = min(max(cu_seqlens[b], 0), total_tokens);
         hi = min(max(cu_seqlens[b + 1], lo), total_tokens);
     }
     float m = -INFINITY, l = 0.f;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (hi > lo) {  // uniform per workgroup
+    if (hi > lo) {  // uniform per wave
         const int s0 = lo / chunk + b;
         const int ns = (hi - 1) / chunk + b - s0 + 1;
-        const size_t slot_floats = (size_t)num_heads * kDV;
-        const float *op = o_part + (size_t)s0 * slot_floats + (size_t)tile * 256 + lane * 4;
+        const size_t slot_elems = (size_t)num_heads * kDV;
+        const PartT *op = o_part + (size_t)s0 * slot_elems + (size_t)tile * 256 + lane * 4;
         const float *mp = m_part + (size_t)s0 * num_heads + head;
         const float *lp = l_part + (size_t)s0 * num_heads + head;
 
-        // slots k0, k0 + 8, ..., k0 + 8 (kU - 1) of this wave
-        auto load = [&](SlotBatch &sb, int k0) {
+        // slots k0, k0 + W, ..., k0 + W (kU - 1)
+        auto load = [&](Batch &sb, int k0) {
 #pragma unroll
             for (int j = 0; j < kU; ++j) {
-                const int s = k0 + kWaves * j;
+                const int s = k0 + W * j;
                 if (s < ns) {
-                    sb.v[j] = *(const floatx4 *)(op + (size_t)s * slot_floats);
+                    sb.v[j] = *(const V *)(op + (size_t)s * slot_elems);
                     sb.m[j] = mp[(size_t)s * num_heads];
                     sb.l[j] = lp[(size_t)s * num_heads];
                 } else {
-                    sb.v[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    sb.v[j] = V{};
                     sb.m[j] = -INFINITY;
                     sb.l[j] = 0.f;
                 }
             }
         };
-        auto merge = [&](const SlotBatch &sb) {
+        auto merge = [&](const Batch &sb) {
             float mx = m;
 #pragma unroll
             for (int j = 0; j < kU; ++j)
@@ -94,53 +116,60 @@ void combine_kernel(const float *__restrict__ o_part,
 #pragma unroll
                 for (int j = 0; j < kU; ++j) {
                     const float e = fast_exp2(sb.m[j] - mx);
-                    acc += e * sb.v[j];
-                    l += e * sb.l[j];
+                    const float el = e * sb.l[j];
+                    acc += (kNorm ? el : e) * to_f32(sb.v[j]);
+                    l += el;
                 }
                 m = mx;
             }
         };
-        constexpr int kStep = kWaves * kU;
-        SlotBatch A, B;
-        int k0 = w;
-        load(A, k0);
-        while (true) {
-            bool more = k0 + kStep < ns;
-            if (more)
-                load(B, k0 + kStep);
-            merge(A);
-            if (!more)
-                break;
-            k0 += kStep;
-            more = k0 + kStep < ns;
-            if (more)
-                load(A, k0 + kStep);
-            merge(B);
-            if (!more)
-                break;
-            k0 += kStep;
+        constexpr int kStep = W * kU;
+        Batch A, B;
+        int k0 = k;
+        if (k0 < ns) {
+            load(A, k0);
+            while (true) {
+                bool more = k0 + kStep < ns;
+                if (more)
+                    load(B, k0 + kStep);
+                merge(A);
+                if (!more)
+                    break;
+                k0 += kStep;
+                more = k0 + kStep < ns;
+                if (more)
+                    load(A, k0 + kStep);
+                merge(B);
+                if (!more)
+                    break;
+                k0 += kStep;
+            }
         }
     }
-    s_m[w][lane] = m;
-    s_l[w][lane] = l;
-    s_o[w][lane] = acc;
-    __syncthreads();
-    if (w == 0) {
-        float mm = s_m[0][lane];
+    if constexpr (W > 1) {
+        s_m[w][lane] = m;
+        s_l[w][lane] = l;
+        s_o[w][lane] = acc;
+        __syncthreads();
+        if (k == 0) {
+            m = s_m[w][lane];
 #pragma unroll
-        for (int k = 1; k < kWaves; ++k)
-            mm = fmaxf(mm, s_m[k][lane]);
-        floatx4 t = {0.f, 0.f, 0.f, 0.f};
-        if (mm != -INFINITY) {
-            float ls = 0.f;
+            for (int j = 1; j < W; ++j)
+                m = fmaxf(m, s_m[w + j][lane]);
+            if (m != -INFINITY) {
+                l = 0.f;
+                acc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int k = 0; k < kWaves; ++k) {
-                const float e = fast_exp2(s_m[k][lane] - mm);
-                ls += e * s_l[k][lane];
-                t += e * s_o[k][lane];
+                for (int j = 0; j < W; ++j) {
+                    const float e = fast_exp2(s_m[w + j][lane] - m);
+                    l += e * s_l[w + j][lane];
+                    acc += e * s_o[w + j][lane];
+                }
             }
-            t *= 1.0f / ls;
         }
+    }
+    if (valid && k == 0) {
+        const floatx4 t = (m != -INFINITY) ? acc * (1.0f / l) : floatx4{0.f, 0.f, 0.f, 0.f};
         const size_t o_off = ((size_t)b * num_heads + head) * kDV + dim0;
         if constexpr (kOutF32) {
             *(floatx4 *)((float *)out + o_off) = t;
@@ -151,18 +180,58 @@ void combine_kernel(const float *__restrict__ o_part,
     }
 }
 
+template <typename PartT, int W, bool kOutF32>
+void launch_w(const Problem &pb, const Plan &p, const Partials &w, int n_items, hipStream_t s)
+{
+    constexpr int kWaves = W > 8 ? W : 8;
+    constexpr int kItems = kWaves / W;
+    hipLaunchKernelGGL((combine_kernel<PartT, W, kOutF32>), dim3((n_items + kItems - 1) / kItems),
+                       dim3(64 * kWaves), 0, s, static_cast<const PartT *>(w.o), w.m, w.l,
+                       pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk, n_items);
+}
+
+template <typename PartT, bool kOutF32>
+void launch_part(const Problem &pb, const Plan &p, const Partials &w, int waves, int n_items,
+                 hipStream_t s)
+{
+    switch (waves) {
+    case 1: launch_w<PartT, 1, kOutF32>(pb, p, w, n_items, s); break;
+    case 2: launch_w<PartT, 2, kOutF32>(pb, p, w, n_items, s); break;
+    case 4: launch_w<PartT, 4, kOutF32>(pb, p, w, n_items, s); break;
+    case 8: launch_w<PartT, 8, kOutF32>(pb, p, w, n_items, s); break;
+    default: launch_w<PartT, 16, kOutF32>(pb, p, w, n_items, s); break;
+    }
+}
+
 }  // namespace
+
+// Waves that share one (tile, sequence) item: enough that each merges about
+// 4 slots of an average sequence, at most 16.
+int combine_waves_per_item(const Plan &p, int batch)
+{
+    const int slots = (p.n_slots + batch - 1) / batch;  // about the slots of one sequence
+    int waves = 1;
+    while (waves < 16 && 4 * waves < slots)
+        waves *= 2;
+    return waves;
+}
 
 hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
                           bool out_fp32, hipStream_t s)
 {
-    const dim3 grid(pb.num_heads / 16 * (kDV / 16), pb.batch), block(64 * kWaves);
-    if (out_fp32)
-        hipLaunchKernelGGL(combine_kernel<true>, grid, block, 0, s, w.o, w.m, w.l,
-                           pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk);
-    else
-        hipLaunchKernelGGL(combine_kernel<false>, grid, block, 0, s, w.o, w.m, w.l,
-                           pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk);
+    const int n_items = pb.num_heads / 16 * (kDV / 16) * pb.batch;
+    const int waves = combine_waves_per_item(p, pb.batch);
+    if (p.part_bytes == 2) {
+        if (out_fp32)
+            launch_part<_Float16, true>(pb, p, w, waves, n_items, s);
+        else
+            launch_part<_Float16, false>(pb, p, w, waves, n_items, s);
+    } else {
+        if (out_fp32)
+            launch_part<float, true>(pb, p, w, waves, n_items, s);
+        else
+            launch_part<float, false>(pb, p, w, waves, n_items, s);
+    }
     return hipGetLastError();
 }
 

@@ -26,14 +26,18 @@ struct Plan {
     int n_chunks;      // splits over the packed tokens
     int n_slots;       // partial-result slots: n_chunks + batch - 1
     int xcd_remap;     // 1: the head tiles of one chunk share an XCD
+    int part_bytes;    // bytes per partial O element: 2 (fp16 path), 4 (fp32 path)
 };
 
-// Partial results of the split kernels (fp32): O unnormalised, n_slots
-// blocks of num_heads x 512 floats each stored as 16 x 16 tiles in MFMA
-// accumulator order (frag_offset in mla_device.hpp); running max in log2
-// units and running sum [n_slots][num_heads].
+// Partial results of the split kernels: O in n_slots blocks of
+// num_heads x 512 elements, each stored as 16 x 16 tiles in MFMA accumulator
+// order (frag_offset in mla_device.hpp), then the running max in log2 units
+// and the running sum [n_slots][num_heads] (fp32). The fp16 path stores O
+// normalised by its running sum, in fp16 (the softmax-weighted mean of the
+// piece's C_N rows, bounded by the largest |C| entry); the fp32 path stores
+// O unnormalised, in fp32.
 struct Partials {
-    float *o;
+    void *o;
     float *m;
     float *l;
 };

@@ -1,8 +1,11 @@
 // fp16 split-KV MLA decode for gfx950:
-//   O*_partial = sum_t 2^(s_t - m) C_N[t],  s_t = log2(e) * scale * (Q* . C[t])
-// for one (chunk of tokens, tile of heads) per workgroup, written as fp32
-// partials (O unnormalised, running max m, running sum l) that
-// mla_combine.hip merges.
+//   O*_partial = sum_t 2^(s_t - m) C_N[t] / l,  l = sum_t 2^(s_t - m),
+//   s_t = log2(e) * scale * (Q* . C[t])
+// for one (chunk of tokens, tile of heads) per workgroup, written as
+// partials (O normalised by l in fp16; running max m and sum l in fp32)
+// that mla_combine.hip merges. Normalised, O is a convex combination of C_N
+// rows, so fp16 holds it at fp16's relative precision whatever the chunk
+// length; the reference's split partials were fp16 as well (unnormalised).
 //
 // Replaces mla_decode_splitk_mma_fp16 (reference
 // csrc/mla_decode_splitk_fwd.cuh:559-892), with a different design:
@@ -45,7 +48,7 @@
 //    global->LDS loads are tracked with explicit vmcnt waits by the waves
 //    that issue them, so a barrier never drains the loads in flight.
 //  * The partial O is stored tile by tile in the MFMA accumulator order
-//    (frag_offset): every store instruction writes 1 KB of contiguous memory.
+//    (frag_offset): every store instruction writes 512 B of contiguous memory.
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
 
@@ -150,7 +153,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
 void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                          const _Float16 *__restrict__ c,
                          const int *__restrict__ cu_seqlens,
-                         float *__restrict__ o_part,
+                         _Float16 *__restrict__ o_part,
                          float *__restrict__ m_part,
                          float *__restrict__ l_part,
                          int num_heads, int batch, int total_tokens, int chunk,
@@ -597,13 +600,23 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                             s_mref[16 * hs + l16] = m_ref[hs];
                 }
                 lds_barrier();  // epilogue barrier of the S waves
-                // ---- epilogue: the unnormalised O of this piece, tile by tile
-                float *obase = o_part + (size_t)slot_out * num_heads * kDV + lane * 4;
+                // ---- epilogue: O of this piece normalised by its running sum
+                // (the halves' sums moved onto the reference max, exactly as
+                // the S waves compute the l they store), in fp16, tile by tile
+                _Float16 *obase = o_part + (size_t)slot_out * num_heads * kDV + lane * 4;
 #pragma unroll
-                for (int hs = 0; hs < T::kNHS; ++hs)
+                for (int hs = 0; hs < T::kNHS; ++hs) {
+                    const int h = 16 * hs + l16;
+                    const float ls = s_l[0][h] * fast_exp2(s_m[0][0][h] - m_ref[hs]) +
+                                     s_l[1][h] * fast_exp2(s_m[0][1][h] - m_ref[hs]);
+                    const float inv = 1.0f / ls;
 #pragma unroll
-                    for (int dt = 0; dt < 8; ++dt)
-                        *(floatx4 *)(obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt)) = o[hs][dt];
+                    for (int dt = 0; dt < 8; ++dt) {
+                        const floatx4 v = o[hs][dt] * inv;
+                        const half4 hv = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+                        *(half4 *)(obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt)) = hv;
+                    }
+                }
             });
         } else {
             // dedicated feeder waves (head tiles of 16 or 32 heads)
@@ -641,7 +654,7 @@ hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStr
     const dim3 grid(p.n_chunks * p.n_head_tiles), block(F16Tile<HT>::kThreads);
     hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr>), grid, block, 0, s,
                        (const _Float16 *)pb.q, (const _Float16 *)pb.c, pb.cu_seqlens,
-                       w.o, w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
+                       static_cast<_Float16 *>(w.o), w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2);
     return hipGetLastError();
 }

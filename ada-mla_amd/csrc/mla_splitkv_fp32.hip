@@ -1,6 +1,7 @@
 // fp32 split-KV MLA decode for gfx950 (the --fp32 path): same math and the
-// same fp32 partial format as the fp16 kernel, on fp32 MFMAs (16x16x4f32) so
-// that products and sums keep fp32 precision end to end.
+// same partial tile layout as the fp16 kernel, with O kept unnormalised in
+// fp32, on fp32 MFMAs (16x16x4f32) so that products and sums keep fp32
+// precision end to end.
 //
 // Replaces mla_decode_fused (reference csrc/mla_decode_fused_fwd.cuh:50-352,
 // launcher csrc/mla_decode_fused_fwd_sm89.cu:6-60), which ran one CTA per 16
@@ -232,7 +233,7 @@ hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p, const Partials 
     const dim3 grid(p.n_chunks * p.n_head_tiles), block(256);
     hipLaunchKernelGGL(splitkv_fp32_kernel, grid, block, 0, s,
                        (const float *)pb.q, (const float *)pb.c, pb.cu_seqlens,
-                       w.o, w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
+                       static_cast<float *>(w.o), w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2);
     return hipGetLastError();
 }

@@ -60,15 +60,16 @@ int mla_last_hip_error(void);
  * (csrc/mla_api.cpp:97). */
 int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits);
 
-/* Workspace for mla_decode_split_fp16 (fp32 split partials). Replaces the
+/* Workspace for mla_decode_split_fp16 (split partials: O normalised by its
+ * running sum in fp16, running max and sum in fp32). Replaces the
  * splits_max / splits_sum / splits_out buffers that mla_decode_split_
  * allocates per call (csrc/mla_api.cpp:71-75). Returns 0 for invalid sizes. */
 size_t mla_decode_split_workspace_size(int num_heads, int seq_length,
                                        int num_splits);
 
 /* fp16 split-KV decode: query [num_heads x 576] fp16, cache [seq_length x 576]
- * fp16 -> out [num_heads x 512] fp16; fp32 accumulation, fp32 softmax state
- * and fp32 partials. Replaces run_mla_decode_splitk<at::Half>
+ * fp16 -> out [num_heads x 512] fp16; fp32 accumulation and softmax state,
+ * fp16 normalised partials merged in fp32. Replaces run_mla_decode_splitk<at::Half>
  * (csrc/mla_decode.hpp:25-34; csrc/mla_decode_splitk_fwd_sm89.cu:26-47 ->
  * run_mla_decode_splitk_fp16, csrc/mla_decode_splitk_fwd.cuh:941-985), which
  * took three caller buffers, no stream, and required num_heads == 128 and
@@ -85,7 +86,7 @@ int mla_decode_split_fp16_ex(const void *query, const void *cache, void *out,
                              unsigned flags, void *stream);
 
 /* The two launches of mla_decode_split_fp16, one at a time: the split-KV
- * kernel, which leaves fp32 partials in the workspace, then the LSE combine,
+ * kernel, which leaves its partials in the workspace, then the LSE combine,
  * which merges them into out. Called back to back on one stream with the
  * same num_heads / seq_length / num_splits they equal mla_decode_split_fp16
  * (the reference's launcher makes the same two launches,
