@@ -38,6 +38,8 @@ _SIGNATURES = {
     "mla_decode_fused_fp32": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "mla_decode_split_batched_workspace_size": (_sz, [_i, _i, _i, _i]),
     "mla_decode_split_batched_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+    "mla_decode_split_bf16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
+    "mla_decode_split_batched_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
 }
 
 _lib = None
@@ -125,22 +127,50 @@ def decode_fused_fp32(q, c, num_splits: int = 0, out=None):
     return out
 
 
-def decode_split_batched_fp16(q, c, cu_seqlens, num_splits: int = 0, out=None):
-    """Batched fp16 decode: q [B, n_h, 576], c [sum N, 576], cu_seqlens [B+1] int32 (device)."""
+def decode_split_bf16(q, c, num_splits: int = 0, out=None):
+    """bf16 decode through mla_decode_split_bf16: q [n_h, 576], c [N, 576]."""
     import torch
     lib = load()
-    assert q.dtype == torch.float16 and c.dtype == torch.float16 and cu_seqlens.dtype == torch.int32
+    assert q.dtype == torch.bfloat16 and c.dtype == torch.bfloat16
+    assert q.is_contiguous() and c.is_contiguous() and q.shape[1] == HEAD_DIM_K and c.shape[1] == HEAD_DIM_K
+    n_h, n = q.shape[0], c.shape[0]
+    if out is None:
+        out = torch.empty((n_h, HEAD_DIM_V), dtype=torch.bfloat16, device=q.device)
+    ws_bytes = lib.mla_decode_split_workspace_size(n_h, n, num_splits)
+    if ws_bytes == 0:
+        raise MlaError("mla_decode_split_workspace_size", STATUS_INVALID_VALUE)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    _check("mla_decode_split_bf16",
+           lib.mla_decode_split_bf16(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                     ws_bytes, n_h, n, num_splits, _stream(q)))
+    return out
+
+
+def decode_split_batched_bf16(q, c, cu_seqlens, num_splits: int = 0, out=None):
+    """Batched bf16 decode (mla_decode_split_batched_bf16); shapes as decode_split_batched_fp16."""
+    return _decode_batched(q, c, cu_seqlens, num_splits, out, "mla_decode_split_batched_bf16")
+
+
+def decode_split_batched_fp16(q, c, cu_seqlens, num_splits: int = 0, out=None):
+    """Batched fp16 decode: q [B, n_h, 576], c [sum N, 576], cu_seqlens [B+1] int32 (device)."""
+    return _decode_batched(q, c, cu_seqlens, num_splits, out, "mla_decode_split_batched_fp16")
+
+
+def _decode_batched(q, c, cu_seqlens, num_splits, out, fn):
+    import torch
+    lib = load()
+    dt = torch.bfloat16 if fn.endswith("bf16") else torch.float16
+    assert q.dtype == dt and c.dtype == dt and cu_seqlens.dtype == torch.int32
     assert q.is_contiguous() and c.is_contiguous() and cu_seqlens.is_contiguous()
     b, n_h = q.shape[0], q.shape[1]
     total = c.shape[0]
     if out is None:
-        out = torch.empty((b, n_h, HEAD_DIM_V), dtype=torch.float16, device=q.device)
+        out = torch.empty((b, n_h, HEAD_DIM_V), dtype=dt, device=q.device)
     ws_bytes = lib.mla_decode_split_batched_workspace_size(b, n_h, total, num_splits)
     if ws_bytes == 0:
         raise MlaError("mla_decode_split_batched_workspace_size", STATUS_INVALID_VALUE)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    _check("mla_decode_split_batched_fp16",
-           lib.mla_decode_split_batched_fp16(q.data_ptr(), c.data_ptr() if total else None,
-                                             cu_seqlens.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
-                                             b, n_h, total, num_splits, _stream(q)))
+    _check(fn, getattr(lib, fn)(q.data_ptr(), c.data_ptr() if total else None, cu_seqlens.data_ptr(),
+                                out.data_ptr(), ws.data_ptr(), ws_bytes, b, n_h, total, num_splits,
+                                _stream(q)))
     return out

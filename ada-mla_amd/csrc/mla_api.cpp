@@ -14,6 +14,9 @@
 //    returned uninitialised memory); mla_decode_fused accepts fp16 as well
 //    (the reference read any dtype as float*, csrc/mla_api.cpp:46-48).
 //  * an optional num_splits keyword (default: chosen from N and the CU count).
+//  * bf16 query/cache are accepted by mla_decode_split, mla_decode_fused and
+//    mla_decode_split_batched (bf16 MFMAs; the reference lists bf16 as
+//    future work, README.md:405-408).
 #include <torch/extension.h>
 
 #include <c10/hip/HIPStream.h>
@@ -34,8 +37,9 @@ void check_status(int st, const char *fn)
 void check_pair(const at::Tensor &query, const at::Tensor &cache, const char *fn)
 {
     TORCH_CHECK(query.scalar_type() == cache.scalar_type(), fn, ": query and cache must have the same dtype");
-    TORCH_CHECK(query.scalar_type() == at::kHalf || query.scalar_type() == at::kFloat, fn,
-                ": dtype must be float16 or float32, got ", query.scalar_type());
+    TORCH_CHECK(query.scalar_type() == at::kHalf || query.scalar_type() == at::kBFloat16 ||
+                    query.scalar_type() == at::kFloat,
+                fn, ": dtype must be float16, bfloat16 or float32, got ", query.scalar_type());
     TORCH_CHECK(cache.dim() == 2 && cache.size(1) == MLA_HEAD_DIM_K, fn, ": cache must be [N, ",
                 MLA_HEAD_DIM_K, "], got ", cache.sizes());
     TORCH_CHECK(cache.size(0) >= 1, fn, ": cache must hold at least one token");
@@ -77,12 +81,13 @@ at::Tensor decode_single(const at::Tensor &query_in, const at::Tensor &cache_in,
     const int splits = static_cast<int>(num_splits);
     at::Tensor out = at::empty({nh, MLA_HEAD_DIM_V}, query.options());
     int st;
-    if (query.scalar_type() == at::kHalf) {
+    if (query.scalar_type() != at::kFloat) {
         const size_t ws_bytes = mla_decode_split_workspace_size(nh, n, splits);
         TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
         at::Tensor ws = workspace(ws_bytes, query);
-        st = mla_decode_split_fp16(query.data_ptr(), cache.data_ptr(), out.data_ptr(), ws.data_ptr(),
-                                   ws_bytes, nh, n, splits, stream_of(query));
+        auto f = query.scalar_type() == at::kHalf ? mla_decode_split_fp16 : mla_decode_split_bf16;
+        st = f(query.data_ptr(), cache.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes, nh, n, splits,
+               stream_of(query));
     } else {
         const size_t ws_bytes = mla_decode_fused_workspace_size(nh, n, splits);
         TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
@@ -114,8 +119,9 @@ at::Tensor mla_decode_split_batched(const at::Tensor &query_in, const at::Tensor
                                     const at::Tensor &cu_seqlens_in, int64_t num_splits)
 {
     const char *fn = "mla_decode_split_batched";
-    TORCH_CHECK(query_in.scalar_type() == at::kHalf && cache_in.scalar_type() == at::kHalf, fn,
-                ": query and cache must be float16");
+    TORCH_CHECK(query_in.scalar_type() == cache_in.scalar_type() &&
+                    (query_in.scalar_type() == at::kHalf || query_in.scalar_type() == at::kBFloat16),
+                fn, ": query and cache must both be float16 or both bfloat16");
     TORCH_CHECK(cu_seqlens_in.scalar_type() == at::kInt && cu_seqlens_in.dim() == 1, fn,
                 ": cu_seqlens must be a 1-D int32 tensor");
     TORCH_CHECK(query_in.dim() == 3 && query_in.size(2) == MLA_HEAD_DIM_K, fn,
@@ -142,9 +148,9 @@ at::Tensor mla_decode_split_batched(const at::Tensor &query_in, const at::Tensor
     const size_t ws_bytes = mla_decode_split_batched_workspace_size(batch, nh, total, splits);
     TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
     at::Tensor ws = workspace(ws_bytes, query);
-    const int st = mla_decode_split_batched_fp16(query.data_ptr(), total > 0 ? cache.data_ptr() : nullptr,
-                                                 cu.data_ptr<int>(), out.data_ptr(), ws.data_ptr(), ws_bytes,
-                                                 batch, nh, total, splits, stream_of(query));
+    auto f = query.scalar_type() == at::kHalf ? mla_decode_split_batched_fp16 : mla_decode_split_batched_bf16;
+    const int st = f(query.data_ptr(), total > 0 ? cache.data_ptr() : nullptr, cu.data_ptr<int>(),
+                     out.data_ptr(), ws.data_ptr(), ws_bytes, batch, nh, total, splits, stream_of(query));
     check_status(st, fn);
     return out;
 }
@@ -154,12 +160,13 @@ at::Tensor mla_decode_split_batched(const at::Tensor &query_in, const at::Tensor
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
 {
     m.doc() = "MI355X (gfx950) MLA decode: drop-in for the ada_mla extension's fused path";
-    m.def("mla_decode_split", &mla_decode_split, "fp16 split-KV MLA decode (query [n_h,576], cache [N,576])",
+    m.def("mla_decode_split", &mla_decode_split,
+          "fp16 / bf16 (or fp32) split-KV MLA decode (query [n_h,576], cache [N,576])",
           pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("num_splits") = 0);
     m.def("mla_decode_fused", &mla_decode_fused, "fp32 MLA decode (query [n_h,576], cache [N,576])",
           pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("num_splits") = 0);
     m.def("mla_decode_split_batched", &mla_decode_split_batched,
-          "batched fp16 MLA decode (query [B,n_h,576], packed cache [sum N,576], cu_seqlens [B+1] int32)",
+          "batched fp16 / bf16 MLA decode (query [B,n_h,576], packed cache [sum N,576], cu_seqlens [B+1] int32)",
           pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("cu_seqlens"),
           pybind11::arg("num_splits") = 0);
     m.attr("HEAD_DIM_C") = MLA_HEAD_DIM_V;

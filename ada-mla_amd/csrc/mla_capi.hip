@@ -178,7 +178,9 @@ constexpr int kPhaseCombine = 2;
 
 // Shared body of every entry point; `phases` selects the split kernel, the
 // combine, or both (in that order, on one stream).
-int run_decode(bool fp32, const void *query, const void *cache, const int *cu_seqlens,
+enum class Dtype { kF16, kBF16, kF32 };
+
+int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seqlens,
                void *out, void *workspace, size_t workspace_bytes, int batch,
                int num_heads, int total_tokens, int num_splits, unsigned flags,
                void *stream, int phases = kPhaseSplit | kPhaseCombine)
@@ -190,6 +192,7 @@ int run_decode(bool fp32, const void *query, const void *cache, const int *cu_se
     if (!aligned16(workspace) || (split && (!aligned16(query) || !aligned16(cache))) ||
         (combine && !aligned16(out)))
         return MLA_STATUS_MISALIGNED;
+    const bool fp32 = dt == Dtype::kF32;
     const Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, current_cu_count());
     if (workspace_bytes < partials_bytes(p, num_heads))
         return MLA_STATUS_WORKSPACE_TOO_SMALL;
@@ -203,6 +206,7 @@ int run_decode(bool fp32, const void *query, const void *cache, const int *cu_se
     pb.num_heads = num_heads;
     pb.total_tokens = total_tokens;
     pb.scale_log2 = scale_log2();
+    pb.bf16 = dt == Dtype::kBF16;
     const Partials w = carve_partials(workspace, p, num_heads);
     hipStream_t s = static_cast<hipStream_t>(stream);
 
@@ -213,7 +217,7 @@ int run_decode(bool fp32, const void *query, const void *cache, const int *cu_se
             return fail_hip(e);
     }
     if (combine) {
-        const hipError_t e = launch_combine(pb, p, w, fp32, s);
+        const hipError_t e = launch_combine(pb, p, w, s);
         if (e != hipSuccess)
             return fail_hip(e);
     }
@@ -263,7 +267,7 @@ int mla_decode_split_fp16_ex(const void *query, const void *cache, void *out,
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return MLA_STATUS_INVALID_VALUE;
-    return mla::run_decode(false, query, cache, nullptr, out, workspace, workspace_bytes, 1,
+    return mla::run_decode(mla::Dtype::kF16, query, cache, nullptr, out, workspace, workspace_bytes, 1,
                            num_heads, seq_length, num_splits, flags, stream);
 }
 
@@ -281,7 +285,7 @@ int mla_decode_split_fp16_partials(const void *query, const void *cache, void *w
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return MLA_STATUS_INVALID_VALUE;
-    return mla::run_decode(false, query, cache, nullptr, nullptr, workspace, workspace_bytes, 1,
+    return mla::run_decode(mla::Dtype::kF16, query, cache, nullptr, nullptr, workspace, workspace_bytes, 1,
                            num_heads, seq_length, num_splits, flags, stream, mla::kPhaseSplit);
 }
 
@@ -290,7 +294,7 @@ int mla_decode_split_fp16_combine(const void *workspace, size_t workspace_bytes,
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return MLA_STATUS_INVALID_VALUE;
-    return mla::run_decode(false, nullptr, nullptr, nullptr, out, const_cast<void *>(workspace),
+    return mla::run_decode(mla::Dtype::kF16, nullptr, nullptr, nullptr, out, const_cast<void *>(workspace),
                            workspace_bytes, 1, num_heads, seq_length, num_splits, 0u, stream,
                            mla::kPhaseCombine);
 }
@@ -310,7 +314,7 @@ int mla_decode_fused_fp32(const float *query, const float *cache, float *out,
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1 || head_dim_c != MLA_HEAD_DIM_K)
         return MLA_STATUS_INVALID_VALUE;
-    return mla::run_decode(true, query, cache, nullptr, out, workspace, workspace_bytes, 1,
+    return mla::run_decode(mla::Dtype::kF32, query, cache, nullptr, out, workspace, workspace_bytes, 1,
                            num_heads, seq_length, num_splits, 0u, stream);
 }
 
@@ -333,8 +337,31 @@ int mla_decode_split_batched_fp16(const void *query, const void *cache, const in
         return MLA_STATUS_INVALID_VALUE;
     if (total_tokens == 0 && !cache)
         cache = query;  // nothing is read from the cache
-    return mla::run_decode(false, query, cache, cu_seqlens, out, workspace, workspace_bytes, batch,
-                           num_heads, total_tokens, num_splits, 0u, stream);
+    return mla::run_decode(mla::Dtype::kF16, query, cache, cu_seqlens, out, workspace, workspace_bytes,
+                           batch, num_heads, total_tokens, num_splits, 0u, stream);
+}
+
+int mla_decode_split_bf16(const void *query, const void *cache, void *out,
+                          void *workspace, size_t workspace_bytes,
+                          int num_heads, int seq_length, int num_splits, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return MLA_STATUS_INVALID_VALUE;
+    return mla::run_decode(mla::Dtype::kBF16, query, cache, nullptr, out, workspace, workspace_bytes, 1,
+                           num_heads, seq_length, num_splits, 0u, stream);
+}
+
+int mla_decode_split_batched_bf16(const void *query, const void *cache, const int *cu_seqlens,
+                                  void *out, void *workspace, size_t workspace_bytes,
+                                  int batch, int num_heads, int total_tokens, int num_splits,
+                                  void *stream)
+{
+    if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0 || !cu_seqlens)
+        return MLA_STATUS_INVALID_VALUE;
+    if (total_tokens == 0 && !cache)
+        cache = query;  // nothing is read from the cache
+    return mla::run_decode(mla::Dtype::kBF16, query, cache, cu_seqlens, out, workspace, workspace_bytes,
+                           batch, num_heads, total_tokens, num_splits, 0u, stream);
 }
 
 }  // extern "C"

@@ -32,7 +32,9 @@ constexpr int kU = 8;  // slots per load batch and wave
 
 template <typename PartT>
 struct SlotBatch {
-    using V = typename std::conditional<sizeof(PartT) == 2, half4, floatx4>::type;
+    using V = typename std::conditional<
+        sizeof(PartT) == 4, floatx4,
+        typename std::conditional<std::is_same<PartT, __bf16>::value, bf16x4, half4>::type>::type;
     V v[kU];
     float m[kU];
     float l[kU];
@@ -43,8 +45,14 @@ __device__ __forceinline__ floatx4 to_f32(const half4 &v)
 {
     return floatx4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
 }
+__device__ __forceinline__ floatx4 to_f32(const bf16x4 &v)
+{
+    return floatx4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
 
-template <typename PartT, int W, bool kOutF32>
+// PartT is the partials' type and the output's: fp16, bf16 (normalised
+// partials) or fp32 (unnormalised).
+template <typename PartT, int W>
 __global__ __launch_bounds__(64 * (W > 8 ? W : 8))
 void combine_kernel(const PartT *__restrict__ o_part,
                     const float *__restrict__ m_part,
@@ -171,35 +179,36 @@ void combine_kernel(const PartT *__restrict__ o_part,
     if (valid && k == 0) {
         const floatx4 t = (m != -INFINITY) ? acc * (1.0f / l) : floatx4{0.f, 0.f, 0.f, 0.f};
         const size_t o_off = ((size_t)b * num_heads + head) * kDV + dim0;
-        if constexpr (kOutF32) {
+        if constexpr (sizeof(PartT) == 4) {
             *(floatx4 *)((float *)out + o_off) = t;
         } else {
-            const half4 h = {(_Float16)t[0], (_Float16)t[1], (_Float16)t[2], (_Float16)t[3]};
-            *(half4 *)((_Float16 *)out + o_off) = h;
+            using V = typename Batch::V;
+            const V h = {(PartT)t[0], (PartT)t[1], (PartT)t[2], (PartT)t[3]};
+            *(V *)((PartT *)out + o_off) = h;
         }
     }
 }
 
-template <typename PartT, int W, bool kOutF32>
+template <typename PartT, int W>
 void launch_w(const Problem &pb, const Plan &p, const Partials &w, int n_items, hipStream_t s)
 {
     constexpr int kWaves = W > 8 ? W : 8;
     constexpr int kItems = kWaves / W;
-    hipLaunchKernelGGL((combine_kernel<PartT, W, kOutF32>), dim3((n_items + kItems - 1) / kItems),
+    hipLaunchKernelGGL((combine_kernel<PartT, W>), dim3((n_items + kItems - 1) / kItems),
                        dim3(64 * kWaves), 0, s, static_cast<const PartT *>(w.o), w.m, w.l,
                        pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk, n_items);
 }
 
-template <typename PartT, bool kOutF32>
+template <typename PartT>
 void launch_part(const Problem &pb, const Plan &p, const Partials &w, int waves, int n_items,
                  hipStream_t s)
 {
     switch (waves) {
-    case 1: launch_w<PartT, 1, kOutF32>(pb, p, w, n_items, s); break;
-    case 2: launch_w<PartT, 2, kOutF32>(pb, p, w, n_items, s); break;
-    case 4: launch_w<PartT, 4, kOutF32>(pb, p, w, n_items, s); break;
-    case 8: launch_w<PartT, 8, kOutF32>(pb, p, w, n_items, s); break;
-    default: launch_w<PartT, 16, kOutF32>(pb, p, w, n_items, s); break;
+    case 1: launch_w<PartT, 1>(pb, p, w, n_items, s); break;
+    case 2: launch_w<PartT, 2>(pb, p, w, n_items, s); break;
+    case 4: launch_w<PartT, 4>(pb, p, w, n_items, s); break;
+    case 8: launch_w<PartT, 8>(pb, p, w, n_items, s); break;
+    default: launch_w<PartT, 16>(pb, p, w, n_items, s); break;
     }
 }
 
@@ -217,21 +226,16 @@ int combine_waves_per_item(const Plan &p, int batch)
 }
 
 hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
-                          bool out_fp32, hipStream_t s)
+                          hipStream_t s)
 {
     const int n_items = pb.num_heads / 16 * (kDV / 16) * pb.batch;
     const int waves = combine_waves_per_item(p, pb.batch);
-    if (p.part_bytes == 2) {
-        if (out_fp32)
-            launch_part<_Float16, true>(pb, p, w, waves, n_items, s);
-        else
-            launch_part<_Float16, false>(pb, p, w, waves, n_items, s);
-    } else {
-        if (out_fp32)
-            launch_part<float, true>(pb, p, w, waves, n_items, s);
-        else
-            launch_part<float, false>(pb, p, w, waves, n_items, s);
-    }
+    if (p.part_bytes == 4)
+        launch_part<float>(pb, p, w, waves, n_items, s);
+    else if (pb.bf16)
+        launch_part<__bf16>(pb, p, w, waves, n_items, s);
+    else
+        launch_part<_Float16>(pb, p, w, waves, n_items, s);
     return hipGetLastError();
 }
 

@@ -8,6 +8,8 @@ namespace mla {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef short shortx4 __attribute__((__vector_size__(4 * sizeof(short))));
 
@@ -21,6 +23,27 @@ __device__ __forceinline__ floatx4 mfma16x16x32(half8 a, half8 b, floatx4 c)
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// The same product with bf16 operands.
+__device__ __forceinline__ floatx4 mfma16x16x32(bf16x8 a, bf16x8 b, floatx4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Vector types of a 16-bit storage type (fp16 or bf16): 8 elements are one
+// MFMA operand, 4 one transpose read or one partial store.
+template <typename E>
+struct Vec;
+template <>
+struct Vec<_Float16> {
+    using v8 = half8;
+    using v4 = half4;
+};
+template <>
+struct Vec<__bf16> {
+    using v8 = bf16x8;
+    using v4 = bf16x4;
+};
+
 // D[16x16] += A[16x4] * B[4x16] in fp32. Lane l supplies A[l % 16][l / 16]
 // and B[l / 16][l % 16]; D layout as above.
 __device__ __forceinline__ floatx4 mfma16x16x4f32(float a, float b, floatx4 c)
@@ -31,11 +54,12 @@ __device__ __forceinline__ floatx4 mfma16x16x4f32(float a, float b, floatx4 c)
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane j points at the
 // 4 halves [row j / 4][4 * (j % 4) .. +3] of a 4 x 16 block; after the read,
 // lane i of the group holds column i of that block (rows 0..3).
-__device__ __forceinline__ half4 lds_read_tr16(const _Float16 *p)
+template <typename E>
+__device__ __forceinline__ typename Vec<E>::v4 lds_read_tr16(const E *p)
 {
-    const MLA_LDS shortx4 *lp = (const MLA_LDS shortx4 *)(const MLA_LDS _Float16 *)p;
+    const MLA_LDS shortx4 *lp = (const MLA_LDS shortx4 *)(const MLA_LDS E *)p;
     shortx4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<MLA_LDS shortx4 *>(lp));
-    return __builtin_bit_cast(half4, r);
+    return __builtin_bit_cast(typename Vec<E>::v4, r);
 }
 
 // 2^x on the hardware exp unit (v_exp_f32); 2^-inf = 0.

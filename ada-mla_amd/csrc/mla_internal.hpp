@@ -32,10 +32,10 @@ struct Plan {
 // Partial results of the split kernels: O in n_slots blocks of
 // num_heads x 512 elements, each stored as 16 x 16 tiles in MFMA accumulator
 // order (frag_offset in mla_device.hpp), then the running max in log2 units
-// and the running sum [n_slots][num_heads] (fp32). The fp16 path stores O
-// normalised by its running sum, in fp16 (the softmax-weighted mean of the
-// piece's C_N rows, bounded by the largest |C| entry); the fp32 path stores
-// O unnormalised, in fp32.
+// and the running sum [n_slots][num_heads] (fp32). The 16-bit paths store O
+// normalised by its running sum, in the input type (fp16 or bf16: the
+// softmax-weighted mean of the piece's C_N rows, bounded by the largest |C|
+// entry); the fp32 path stores O unnormalised, in fp32.
 struct Partials {
     void *o;
     float *m;
@@ -51,6 +51,7 @@ struct Problem {
     int num_heads;
     int total_tokens;
     float scale_log2;       // softmax scale * log2(e)
+    bool bf16;              // 16-bit path: q, c, out (and the partial O) in bf16, not fp16
 };
 
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
@@ -62,7 +63,9 @@ hipError_t launch_splitkv_fp16(const Problem &pb, const Plan &p,
                                const Partials &w, bool tr_load, hipStream_t s);
 hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p,
                                const Partials &w, hipStream_t s);
+// The output has the partials' type: fp16 / bf16 on the 16-bit path, fp32
+// on the fp32 path.
 hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
-                          bool out_fp32, hipStream_t s);
+                          hipStream_t s);
 
 }  // namespace mla

@@ -134,7 +134,7 @@ __device__ __forceinline__ void lds_barrier()
 // MLA_WAIT_VMCNT; the compiler's own vmcnt waits stay correct because
 // vector-memory loads retire in order, so loads it does not count only make
 // its waits more conservative.
-__device__ __forceinline__ void global_to_lds16(const _Float16 *base, int off, const void *lds)
+__device__ __forceinline__ void global_to_lds16(const void *base, int off, const void *lds)
 {
     const unsigned l = __builtin_amdgcn_readfirstlane(
         (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
@@ -148,20 +148,22 @@ __device__ __forceinline__ void global_to_lds16(const _Float16 *base, int off, c
                  : "=&s"(saved_m0) : "v"(off), "s"(base), "s"(l) : "memory");
 }
 
-template <int HT, bool kTr>
+template <int HT, bool kTr, typename E>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
-void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
-                         const _Float16 *__restrict__ c,
+void splitkv_fp16_kernel(const E *__restrict__ q,
+                         const E *__restrict__ c,
                          const int *__restrict__ cu_seqlens,
-                         _Float16 *__restrict__ o_part,
+                         E *__restrict__ o_part,
                          float *__restrict__ m_part,
                          float *__restrict__ l_part,
                          int num_heads, int batch, int total_tokens, int chunk,
                          int n_head_tiles, int xcd_remap, float scale_log2)
 {
     using T = F16Tile<HT>;
-    __shared__ __attribute__((aligned(1024))) _Float16 s_ring[T::kRing * T::kSlot];
-    __shared__ __attribute__((aligned(16))) _Float16 s_p[2][HT * T::kPRow];
+    using E8 = typename Vec<E>::v8;
+    using E4 = typename Vec<E>::v4;
+    __shared__ __attribute__((aligned(1024))) E s_ring[T::kRing * T::kSlot];
+    __shared__ __attribute__((aligned(16))) E s_p[2][HT * T::kPRow];
     __shared__ float s_m[2][2][HT];  // [P buffer][token half][head]: running max of the half
     __shared__ float s_l[2][HT];     // [token half][head]: running sum at the end of a piece
     __shared__ float s_mref[HT];     // [head]: the O accumulators' reference max at the end of a piece
@@ -234,13 +236,13 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
     // recomputed at each load (a few VALU ops) instead of being kept live,
     // or spilled, across the piece: a spill reload here would make the
     // compiler wait for every outstanding global->LDS load.
-    auto dma_row = [&](const _Float16 *base, int lim, int slot, int row) {
+    auto dma_row = [&](const E *base, int lim, int slot, int row) {
         int ln = lane;
         asm volatile("" : "+v"(ln));
         global_to_lds16(base, min(row, lim) * (kDK * 2) + 16 * (ln ^ row_swizzle(row)),
                         s_ring + slot * T::kSlot + row * kDV);
     };
-    auto dma_rope = [&](const _Float16 *base, int lim, int slot, int ru) {
+    auto dma_rope = [&](const E *base, int lim, int slot, int ru) {
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const int rrow = 8 * ru + (ln >> 3);
@@ -253,7 +255,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
     // 0..kPre-1. Each wave waits for its own loads; the barrier after this
     // (A) then publishes Q* and those blocks to every wave.
     auto prologue_loads = [&](int b, int p_lo, int p_hi) {
-        const _Float16 *qb = q + ((size_t)b * num_heads + head0) * kDK;
+        const E *qb = q + ((size_t)b * num_heads + head0) * kDK;
 #pragma unroll
         for (int j = 0; j < T::kQBlocks; ++j) {
 #pragma unroll
@@ -295,9 +297,9 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
         for (int j = 0; j < 2; ++j)
             a_off[4 + j] = T::kRope + 8 * ((4 * j + g) ^ rope_swizzle(l16));
         // operand of K-step kk of row r of a slot
-        auto a_at = [&](const _Float16 *slot, int r, int kk) -> half8 {
-            return kk < 16 ? *(const half8 *)(slot + r * kDV + a_off[kk & 3] + 128 * (kk >> 2))
-                           : *(const half8 *)(slot + r * (kDK - kDV) + a_off[kk - 12]);
+        auto a_at = [&](const E *slot, int r, int kk) -> E8 {
+            return kk < 16 ? *(const E8 *)(slot + r * kDV + a_off[kk & 3] + 128 * (kk >> 2))
+                           : *(const E8 *)(slot + r * (kDK - kDV) + a_off[kk - 12]);
         };
 
         for_each_piece([&](int b, int p_lo, int p_hi) {
@@ -309,13 +311,13 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
             // Q* fragments (B operand of S^T = C Q*^T): lane holds head
             // kSH*hg + 16*ns + l16 of the tile, dims 32*kk + 8*g .. +7. Q*
             // rows sit in the ring in the same swizzled layout as C rows.
-            half8 qf[T::kNS][kDK / 32];
+            E8 qf[T::kNS][kDK / 32];
             {
                 // head h of the tile is row h % 32 of Q* slot kPre + h / 32
 #pragma unroll
                 for (int ns = 0; ns < T::kNS; ++ns) {
                     const int h = T::kSH * hg + 16 * ns + l16;
-                    const _Float16 *qs = s_ring + (T::kPre + h / 32) * T::kSlot;
+                    const E *qs = s_ring + (T::kPre + h / 32) * T::kSlot;
 #pragma unroll
                     for (int kk = 0; kk < kDK / 32; ++kk)
                         qf[ns][kk] = a_at(qs, h % 32, kk);
@@ -333,7 +335,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                 if (t + 1 < nblk) {
                     const int blk = t + 1;
                     const int t0 = p_lo + blk * T::kBT + 16 * th;
-                    const _Float16 *cslot = s_ring + (blk % T::kRing) * T::kSlot;
+                    const E *cslot = s_ring + (blk % T::kRing) * T::kSlot;
                     // ---- S^T tiles: tokens t0 + (0..15), heads of this wave.
                     // The 18 operand reads go out in batches of 3 K-steps,
                     // two batches ahead of the MFMAs that consume them.
@@ -345,7 +347,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                             acc[ns][j] = floatx4{0.f, 0.f, 0.f, 0.f};
                     constexpr int kB = 3;                 // K-steps per batch
                     constexpr int kNB = kDK / 32 / kB;    // batches (6)
-                    half8 ab[3][kB];
+                    E8 ab[3][kB];
                     auto load_batch = [&](int buf, int k0) {
 #pragma unroll
                         for (int k = 0; k < kB; ++k)
@@ -389,17 +391,17 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                         const float ref = mn == -INFINITY ? 0.f : mn;
                         const float alpha = fast_exp2(m_run[ns] - ref);
                         m_run[ns] = mn;
-                        half4 ph;
+                        E4 ph;
                         float ps = 0.f;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const float p = fast_exp2(sv[i] - ref);
                             ps += p;
-                            ph[i] = (_Float16)p;
+                            ph[i] = (E)p;
                         }
                         l_lane[ns] = l_lane[ns] * alpha + ps;
                         const int hrow = T::kSH * hg + 16 * ns + l16;
-                        *(half4 *)(s_p[blk & 1] + hrow * T::kPRow + 16 * th + 4 * g) = ph;
+                        *(E4 *)(s_p[blk & 1] + hrow * T::kPRow + 16 * th + 4 * g) = ph;
                         if (g == 0)
                             s_m[blk & 1][th][hrow] = mn;
                     }
@@ -442,7 +444,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
         const int feeder = T::kOFeeds ? wave - T::kOWave0 : wave - T::kSWaves;
         // unit k (0..kFeedUnits-1) of this feeder's share of a block: C_N
         // row kFeedRows*feeder + k, or a rope unit of those rows
-        auto load_unit = [&](const _Float16 *base, int lim, int slot, int k) {
+        auto load_unit = [&](const E *base, int lim, int slot, int k) {
             if (k < T::kFeedRows)
                 dma_row(base, lim, slot, T::kFeedRows * feeder + k);
             else
@@ -474,17 +476,17 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
             if constexpr (T::kOFeeds)
                 __builtin_amdgcn_s_setprio(2);
             // C_N^T operand of dims 128*ow + 16*dt .. +15 from a ring slot
-            auto load_av = [&](const _Float16 *cs, int dt) -> half8 {
+            auto load_av = [&](const E *cs, int dt) -> E8 {
                 if constexpr (kTr) {
                     // lane (g, j): rows 8g + j/4 (+4), dims 128*ow + 16*dt + 4*(j%4) .. +3
                     const int r0 = 8 * g + (l16 >> 2);
                     const int cl = 16 * ow + 2 * dt + ((l16 & 3) >> 1);
                     const int sub = 4 * (l16 & 1);
-                    const half4 lo4 = lds_read_tr16(cs + r0 * kDV + 8 * (cl ^ row_swizzle(r0)) + sub);
-                    const half4 hi4 = lds_read_tr16(cs + (r0 + 4) * kDV + 8 * (cl ^ row_swizzle(r0 + 4)) + sub);
-                    return half8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                    const E4 lo4 = lds_read_tr16<E>(cs + r0 * kDV + 8 * (cl ^ row_swizzle(r0)) + sub);
+                    const E4 hi4 = lds_read_tr16<E>(cs + (r0 + 4) * kDV + 8 * (cl ^ row_swizzle(r0 + 4)) + sub);
+                    return E8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
                 } else {
-                    half8 v;
+                    E8 v;
                     const int col = 128 * ow + 16 * dt + l16;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
@@ -523,7 +525,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                 // C_N^T fragments of the block the next step accumulates; each
                 // step reloads them for its successor right after the MFMAs
                 // that consume them
-                half8 av[8];
+                E8 av[8];
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt)
                     av[dt] = load_av(s_ring, dt);
@@ -538,13 +540,13 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                         // of the half this lane feeds (tokens 8g..8g+7: half
                         // g/2) is scaled onto it, the accumulator moves by
                         // 2^(M_old - M)
-                        half8 pb[T::kNHS];
+                        E8 pb[T::kNHS];
                         float m0[T::kNHS], m1[T::kNHS];
 #pragma unroll
                         for (int hs = 0; hs < T::kNHS; ++hs) {
                             m0[hs] = s_m[blk & 1][0][16 * hs + l16];
                             m1[hs] = s_m[blk & 1][1][16 * hs + l16];
-                            pb[hs] = *(const half8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
+                            pb[hs] = *(const E8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
                         }
                         // The reference only moves when a max passes it by more
                         // than kLazyRescale (P scaled onto it then stays <= 2^8,
@@ -559,7 +561,17 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                             moved |= up;
                             if (up)
                                 m_ref[hs] = mn;
-                            pb[hs] *= (_Float16)fast_exp2((g < 2 ? m0[hs] : m1[hs]) - m_ref[hs]);
+                            const float f = fast_exp2((g < 2 ? m0[hs] : m1[hs]) - m_ref[hs]);
+                            if constexpr (__is_same(E, _Float16)) {
+                                pb[hs] *= (E)f;
+                            } else {
+                                // bf16: scale in fp32, so that the factor is not
+                                // itself rounded to 8 bits (one error for the
+                                // whole half-block)
+#pragma unroll
+                                for (int i = 0; i < 8; ++i)
+                                    pb[hs][i] = (E)((float)pb[hs][i] * f);
+                            }
                         }
                         if (__builtin_amdgcn_ballot_w64(moved) != 0) {
 #pragma unroll
@@ -572,7 +584,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                         // the next block's operand reads (and, when the O
                         // waves feed, this step's global->LDS loads) placed
                         // between the MFMAs
-                        const _Float16 *cn = s_ring + ((blk + 1) % T::kRing) * T::kSlot;
+                        const E *cn = s_ring + ((blk + 1) % T::kRing) * T::kSlot;
 #pragma unroll
                         for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
@@ -603,7 +615,7 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
                 // ---- epilogue: O of this piece normalised by its running sum
                 // (the halves' sums moved onto the reference max, exactly as
                 // the S waves compute the l they store), in fp16, tile by tile
-                _Float16 *obase = o_part + (size_t)slot_out * num_heads * kDV + lane * 4;
+                E *obase = o_part + (size_t)slot_out * num_heads * kDV + lane * 4;
 #pragma unroll
                 for (int hs = 0; hs < T::kNHS; ++hs) {
                     const int h = 16 * hs + l16;
@@ -613,8 +625,8 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
 #pragma unroll
                     for (int dt = 0; dt < 8; ++dt) {
                         const floatx4 v = o[hs][dt] * inv;
-                        const half4 hv = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-                        *(half4 *)(obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt)) = hv;
+                        const E4 hv = {(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
+                        *(E4 *)(obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt)) = hv;
                     }
                 }
             });
@@ -648,15 +660,25 @@ void splitkv_fp16_kernel(const _Float16 *__restrict__ q,
     }
 }
 
-template <int HT, bool kTr>
+template <int HT, bool kTr, typename E>
 hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStream_t s)
 {
     const dim3 grid(p.n_chunks * p.n_head_tiles), block(F16Tile<HT>::kThreads);
-    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr>), grid, block, 0, s,
-                       (const _Float16 *)pb.q, (const _Float16 *)pb.c, pb.cu_seqlens,
-                       static_cast<_Float16 *>(w.o), w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
+    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E>), grid, block, 0, s,
+                       (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens,
+                       static_cast<E *>(w.o), w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2);
     return hipGetLastError();
+}
+
+template <typename E>
+hipError_t launch_e(const Problem &pb, const Plan &p, const Partials &w, bool tr_load, hipStream_t s)
+{
+    switch (p.head_tile) {
+    case 64: return tr_load ? launch_ht<64, true, E>(pb, p, w, s) : launch_ht<64, false, E>(pb, p, w, s);
+    case 32: return tr_load ? launch_ht<32, true, E>(pb, p, w, s) : launch_ht<32, false, E>(pb, p, w, s);
+    default: return tr_load ? launch_ht<16, true, E>(pb, p, w, s) : launch_ht<16, false, E>(pb, p, w, s);
+    }
 }
 
 }  // namespace
@@ -666,11 +688,7 @@ hipError_t launch_splitkv_fp16(const Problem &pb, const Plan &p, const Partials 
 {
     if (p.n_chunks == 0)
         return hipSuccess;
-    switch (p.head_tile) {
-    case 64: return tr_load ? launch_ht<64, true>(pb, p, w, s) : launch_ht<64, false>(pb, p, w, s);
-    case 32: return tr_load ? launch_ht<32, true>(pb, p, w, s) : launch_ht<32, false>(pb, p, w, s);
-    default: return tr_load ? launch_ht<16, true>(pb, p, w, s) : launch_ht<16, false>(pb, p, w, s);
-    }
+    return pb.bf16 ? launch_e<__bf16>(pb, p, w, tr_load, s) : launch_e<_Float16>(pb, p, w, tr_load, s);
 }
 
 }  // namespace mla

@@ -45,6 +45,7 @@ WORKLOADS = {
     "batched": dict(kind="batched", n_h=128, batch=32,
                     desc="fp16 batched, B=32, N_b ~ U[512,16384] seed 42 (BASELINE config 5)"),
     "fp32": dict(kind="fp32", n_h=128, n=1024, desc="fp32 path, n_h=128, N=1024 (BASELINE config 1 shape on GPU)"),
+    "bf16": dict(kind="bf16", n_h=128, n=4096, desc="bf16 KV cache, n_h=128, N=4096 (bf16 variant of config 2)"),
 }
 
 
@@ -192,7 +193,7 @@ def main():
     else:
         batch, total = 1, wl["n"]
         q_shape, c_shape = (n_h, 576), (total, 576)
-        dtype = torch.float32 if kind == "fp32" else torch.float16
+        dtype = {"fp32": torch.float32, "bf16": torch.bfloat16}.get(kind, torch.float16)
     esz = 4 if dtype == torch.float32 else 2
     pair_bytes = (math.prod(q_shape) + math.prod(c_shape)) * esz
     pool = max(2, math.ceil(args.flush_mb * 2**20 / pair_bytes))
@@ -201,7 +202,7 @@ def main():
     out = torch.empty((batch, n_h, 512) if kind == "batched" else (n_h, 512), device=dev, dtype=dtype)
 
     splits = args.num_splits
-    if kind == "fp16":
+    if kind in ("fp16", "bf16"):
         ws_bytes = lib.mla_decode_split_workspace_size(n_h, total, splits)
         eff_splits = lib.mla_decode_split_num_splits(n_h, total, splits)
     elif kind == "fp32":
@@ -221,6 +222,9 @@ def main():
         if kind == "fp16":
             check(lib.mla_decode_split_fp16_partials(q.data_ptr(), c.data_ptr(), ws.data_ptr(), ws_bytes,
                                                      n_h, total, splits, 0, sptr), "partials")
+        elif kind == "bf16":
+            check(lib.mla_decode_split_bf16(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                                            n_h, total, splits, sptr), "bf16")
         elif kind == "fp32":
             check(lib.mla_decode_fused_fp32(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
                                             n_h, 576, total, splits, sptr), "fused_fp32")
@@ -293,7 +297,7 @@ def main():
     roof.update({
         "traffic": traffic,
         "traffic_source": traffic_src,
-        "kernel": "splitkv_fp16_kernel" if kind in ("fp16", "batched") else "splitkv_fp32_kernel",
+        "kernel": "splitkv_fp32_kernel" if kind == "fp32" else "splitkv_fp16_kernel",
         "kernel_us": k_us,
         "kernel_us_event_pair_median": k_pair_us,
         "algorithmic_bytes": alg_bytes,
@@ -303,8 +307,8 @@ def main():
         "roofline_time_us": max(bound_hbm, bound_mfma),
         "call_frac": max(bound_hbm, bound_mfma) / us_call,
     })
-    if kind == "batched":
-        roof["note"] = "batched has no phase split: kernel_us is the whole call"
+    if kind in ("batched", "bf16"):
+        roof["note"] = f"{kind} has no phase split: kernel_us is the whole call"
 
     res = {
         "metric": METRIC,
@@ -317,7 +321,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32" if kind == "fp32" else "fp16",
+        "dtype": {"fp32": "fp32", "bf16": "bf16"}.get(kind, "fp16"),
         "data": "synthetic (N(0,1), torch generator seed 42, resident in HBM)",
         "config": {
             "workload": wl["desc"],

@@ -136,6 +136,21 @@ int mla_decode_split_batched_fp16(const void *query, const void *cache,
                                   int batch, int num_heads, int total_tokens,
                                   int num_splits, void *stream);
 
+/* bf16 KV cache: mla_decode_split_fp16 and mla_decode_split_batched_fp16
+ * with query, cache and out in bf16 (the same workspace sizes; bf16 MFMAs,
+ * fp32 accumulation and softmax state, P and the normalised partials in
+ * bf16). No reference counterpart: the reference lists bf16 as future work
+ * (README.md:405-408) and its --bf16 flag is commented out (mla.py:163). */
+int mla_decode_split_bf16(const void *query, const void *cache, void *out,
+                          void *workspace, size_t workspace_bytes,
+                          int num_heads, int seq_length, int num_splits,
+                          void *stream);
+int mla_decode_split_batched_bf16(const void *query, const void *cache,
+                                  const int *cu_seqlens, void *out,
+                                  void *workspace, size_t workspace_bytes,
+                                  int batch, int num_heads, int total_tokens,
+                                  int num_splits, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -80,6 +80,8 @@ FAKE = 0x10000  # never dereferenced: every call below returns before any launch
 ])
 def test_split_fp16_argument_errors(args, code):
     assert capi.load().mla_decode_split_fp16(*args) == code
+    # the bf16 entry takes the same arguments and validates them the same way
+    assert capi.load().mla_decode_split_bf16(*args) == code
 
 
 def test_fused_fp32_rejects_head_dim():
@@ -90,9 +92,10 @@ def test_fused_fp32_rejects_head_dim():
         capi.STATUS_WORKSPACE_TOO_SMALL
 
 
-def test_batched_argument_errors():
+@pytest.mark.parametrize("fn", ["mla_decode_split_batched_fp16", "mla_decode_split_batched_bf16"])
+def test_batched_argument_errors(fn):
     lib = capi.load()
-    f = lib.mla_decode_split_batched_fp16
+    f = getattr(lib, fn)
     assert f(FAKE, FAKE, None, FAKE, FAKE, 1 << 30, 4, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
     assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30, 0, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
     assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 16, 4, 128, 100, 0, None) == capi.STATUS_WORKSPACE_TOO_SMALL
@@ -114,7 +117,8 @@ def test_extension_surface():
 
 @pytest.mark.parametrize("q,c,msg", [
     (torch.zeros(128, 576, dtype=torch.float16), torch.zeros(64, 576, dtype=torch.float32), "same dtype"),
-    (torch.zeros(128, 576, dtype=torch.bfloat16), torch.zeros(64, 576, dtype=torch.bfloat16), "float16 or float32"),
+    (torch.zeros(128, 576, dtype=torch.float64), torch.zeros(64, 576, dtype=torch.float64),
+     "float16, bfloat16 or float32"),
     (torch.zeros(128, 576, dtype=torch.float16), torch.zeros(64, 577, dtype=torch.float16), "cache must be"),
     (torch.zeros(128, 576, dtype=torch.float16), torch.zeros(0, 576, dtype=torch.float16), "at least one token"),
     (torch.zeros(128, 512, dtype=torch.float16), torch.zeros(64, 576, dtype=torch.float16), "query must be"),
@@ -138,3 +142,5 @@ def test_batched_extension_rejects_bad_inputs():
         m.mla_decode_split_batched(q, c, torch.zeros(3, dtype=torch.int64))
     with pytest.raises(RuntimeError, match="GPU tensors"):
         m.mla_decode_split_batched(q, c, torch.zeros(3, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="both bfloat16"):
+        m.mla_decode_split_batched(q.bfloat16(), c, torch.zeros(3, dtype=torch.int32))
