@@ -40,6 +40,9 @@ _SIGNATURES = {
     "mla_decode_split_batched_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "mla_decode_split_bf16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "mla_decode_split_batched_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+    "mla_decode_paged_workspace_size": (_sz, [_i, _i, _i, _i]),
+    "mla_decode_paged_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "mla_decode_paged_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _i, _vp]),
 }
 
 _lib = None
@@ -173,4 +176,28 @@ def _decode_batched(q, c, cu_seqlens, num_splits, out, fn):
     _check(fn, getattr(lib, fn)(q.data_ptr(), c.data_ptr() if total else None, cu_seqlens.data_ptr(),
                                 out.data_ptr(), ws.data_ptr(), ws_bytes, b, n_h, total, num_splits,
                                 _stream(q)))
+    return out
+
+
+def decode_paged(q, kv_cache, block_table, cu_seqlens, total_tokens: int, num_splits: int = 0, out=None):
+    """Paged-KV decode (mla_decode_paged_fp16 / _bf16 by q's dtype): q [B, n_h, 576],
+    kv_cache [num_pages, page_size, 576], block_table [B, max_pages] int32,
+    cu_seqlens [B+1] int32 (device), total_tokens = cu_seqlens[B] (host)."""
+    import torch
+    lib = load()
+    assert q.dtype in (torch.float16, torch.bfloat16) and kv_cache.dtype == q.dtype
+    assert block_table.dtype == torch.int32 and cu_seqlens.dtype == torch.int32
+    assert q.is_contiguous() and kv_cache.is_contiguous() and block_table.is_contiguous()
+    b, n_h = q.shape[0], q.shape[1]
+    num_pages, page_size = kv_cache.shape[0], kv_cache.shape[1]
+    if out is None:
+        out = torch.empty((b, n_h, HEAD_DIM_V), dtype=q.dtype, device=q.device)
+    ws_bytes = lib.mla_decode_paged_workspace_size(b, n_h, total_tokens, num_splits)
+    if ws_bytes == 0:
+        raise MlaError("mla_decode_paged_workspace_size", STATUS_INVALID_VALUE)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    fn = "mla_decode_paged_fp16" if q.dtype == torch.float16 else "mla_decode_paged_bf16"
+    _check(fn, getattr(lib, fn)(q.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), cu_seqlens.data_ptr(),
+                                out.data_ptr(), ws.data_ptr(), ws_bytes, b, n_h, total_tokens, page_size,
+                                num_pages, block_table.shape[1], num_splits, _stream(q)))
     return out

@@ -47,3 +47,31 @@ def batched_inputs(num_heads: int, seqlens, seed: int = 42, dtype=np.float16):
     q = normal((batch, num_heads, HEAD_DIM_K), seed, dtype)
     c = normal((int(cu[-1]), HEAD_DIM_K), seed + 1, dtype)
     return q, c, cu
+
+
+def paged_inputs(num_heads: int, seqlens, page_size: int, seed: int = 42, dtype=np.float16,
+                 spare_pages: int = 3, spare_columns: int = 2):
+    """A paged cache holding the same logical data as batched_inputs(num_heads,
+    seqlens, seed, dtype): Q* [B, num_heads, 576], kv_pages
+    [num_pages, page_size, 576], block_table [B, max_pages + spare_columns]
+    (int32; every sequence's pages are a random permutation of the pool, the
+    spare columns and pages are filled with values no sequence reads),
+    cu_seqlens [B + 1] (int32), and the packed cache itself."""
+    q, c, cu = batched_inputs(num_heads, seqlens, seed, dtype)
+    seqlens = np.diff(cu.astype(np.int64))
+    need = [-(-int(n) // page_size) for n in seqlens]
+    n_pages = sum(need) + spare_pages
+    rng = np.random.Generator(np.random.PCG64(seed + 2000))
+    perm = rng.permutation(n_pages)
+    kv = normal((n_pages, page_size, HEAD_DIM_K), seed + 3, dtype)  # unread rows keep random data
+    cols = max(need + [1]) + spare_columns
+    bt = np.full((len(seqlens), cols), n_pages + 7, dtype=np.int32)  # out-of-range: never read
+    k = 0
+    for b, n in enumerate(seqlens):
+        for j in range(need[b]):
+            page = int(perm[k])
+            k += 1
+            bt[b, j] = page
+            rows = c[cu[b] + j * page_size: cu[b] + min((j + 1) * page_size, int(n))]
+            kv[page, :rows.shape[0]] = rows
+    return q, kv, bt, cu, c

@@ -155,6 +155,64 @@ at::Tensor mla_decode_split_batched(const at::Tensor &query_in, const at::Tensor
     return out;
 }
 
+// No reference counterpart: a paged KV cache [num_pages, page_size, 576]
+// addressed through block_table [batch, max_pages] (int32), with the
+// sequences' lengths as prefix sums cu_seqlens [batch + 1] (int32).
+// total_tokens (= cu_seqlens[batch]) is read from the device when not given,
+// which synchronises the stream.
+at::Tensor mla_decode_paged(const at::Tensor &query_in, const at::Tensor &kv_in,
+                            const at::Tensor &block_table_in, const at::Tensor &cu_seqlens_in,
+                            int64_t total_tokens, int64_t num_splits)
+{
+    const char *fn = "mla_decode_paged";
+    TORCH_CHECK(query_in.scalar_type() == kv_in.scalar_type() &&
+                    (query_in.scalar_type() == at::kHalf || query_in.scalar_type() == at::kBFloat16),
+                fn, ": query and kv_cache must both be float16 or both bfloat16");
+    TORCH_CHECK(block_table_in.scalar_type() == at::kInt && block_table_in.dim() == 2, fn,
+                ": block_table must be a 2-D int32 tensor");
+    TORCH_CHECK(cu_seqlens_in.scalar_type() == at::kInt && cu_seqlens_in.dim() == 1, fn,
+                ": cu_seqlens must be a 1-D int32 tensor");
+    TORCH_CHECK(query_in.dim() == 3 && query_in.size(2) == MLA_HEAD_DIM_K, fn,
+                ": query must be [batch, num_heads, ", MLA_HEAD_DIM_K, "], got ", query_in.sizes());
+    TORCH_CHECK(kv_in.dim() == 3 && kv_in.size(2) == MLA_HEAD_DIM_K && kv_in.size(0) >= 1, fn,
+                ": kv_cache must be [num_pages >= 1, page_size, ", MLA_HEAD_DIM_K, "], got ", kv_in.sizes());
+    const int64_t page = kv_in.size(1);
+    TORCH_CHECK(page >= 32 && (page & (page - 1)) == 0, fn, ": page_size must be a power of two >= 32, got ",
+                page);
+    TORCH_CHECK(kv_in.size(0) <= INT32_MAX, fn, ": too many pages");
+    const int64_t batch = query_in.size(0);
+    TORCH_CHECK(batch >= 1 && cu_seqlens_in.size(0) == batch + 1 && block_table_in.size(0) == batch, fn,
+                ": cu_seqlens must have batch + 1 entries and block_table batch rows");
+    TORCH_CHECK(block_table_in.size(1) >= 1, fn, ": block_table needs at least one column");
+    check_heads(query_in.size(1), fn);
+    TORCH_CHECK(query_in.is_cuda() && kv_in.is_cuda() && block_table_in.is_cuda() && cu_seqlens_in.is_cuda(), fn,
+                ": all inputs must be GPU tensors");
+    TORCH_CHECK(query_in.device() == kv_in.device() && query_in.device() == block_table_in.device() &&
+                    query_in.device() == cu_seqlens_in.device(),
+                fn, ": all inputs must be on the same device");
+    const at::OptionalDeviceGuard guard(query_in.device());
+    const at::Tensor query = query_in.contiguous();
+    const at::Tensor kv = kv_in.contiguous();
+    const at::Tensor bt = block_table_in.contiguous();
+    const at::Tensor cu = cu_seqlens_in.contiguous();
+    if (total_tokens < 0)
+        total_tokens = cu[batch].item<int>();
+    TORCH_CHECK(total_tokens >= 0 && total_tokens <= INT32_MAX, fn, ": bad total_tokens ", total_tokens);
+    const int nh = static_cast<int>(query.size(1));
+    const int total = static_cast<int>(total_tokens);
+    const int splits = static_cast<int>(num_splits);
+    at::Tensor out = at::empty({batch, nh, MLA_HEAD_DIM_V}, query.options());
+    const size_t ws_bytes = mla_decode_paged_workspace_size(static_cast<int>(batch), nh, total, splits);
+    TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
+    at::Tensor ws = workspace(ws_bytes, query);
+    auto f = query.scalar_type() == at::kHalf ? mla_decode_paged_fp16 : mla_decode_paged_bf16;
+    const int st = f(query.data_ptr(), kv.data_ptr(), bt.data_ptr<int>(), cu.data_ptr<int>(), out.data_ptr(),
+                     ws.data_ptr(), ws_bytes, static_cast<int>(batch), nh, total, static_cast<int>(page),
+                     static_cast<int>(kv.size(0)), static_cast<int>(bt.size(1)), splits, stream_of(query));
+    check_status(st, fn);
+    return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
@@ -169,6 +227,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
           "batched fp16 / bf16 MLA decode (query [B,n_h,576], packed cache [sum N,576], cu_seqlens [B+1] int32)",
           pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("cu_seqlens"),
           pybind11::arg("num_splits") = 0);
+    m.def("mla_decode_paged", &mla_decode_paged,
+          "paged-KV fp16 / bf16 MLA decode (query [B,n_h,576], kv_cache [pages,page_size,576], "
+          "block_table [B,max_pages] int32, cu_seqlens [B+1] int32)",
+          pybind11::arg("query"), pybind11::arg("kv_cache"), pybind11::arg("block_table"),
+          pybind11::arg("cu_seqlens"), pybind11::arg("total_tokens") = -1, pybind11::arg("num_splits") = 0);
     m.attr("HEAD_DIM_C") = MLA_HEAD_DIM_V;
     m.attr("HEAD_DIM_ROPE") = MLA_HEAD_DIM_K - MLA_HEAD_DIM_V;
     m.attr("HEAD_DIM_K") = MLA_HEAD_DIM_K;

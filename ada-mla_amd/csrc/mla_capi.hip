@@ -79,12 +79,12 @@ void set_chunks(Plan &p, int total_tokens, int batch, int w)
 // the combine) at ~8 TB/s and the combine's memory round trips. Head tiles
 // that share a chunk but not an XCD re-read C from HBM, which the model
 // charges as slower steps.
-double modelled_us(const Plan &p, int num_heads, int batch, int cu_count)
+double modelled_us(const Plan &p, int num_heads, int batch, int cu_count, bool paged)
 {
     const double step_us = p.head_tile == 64 ? 1.5 : p.head_tile == 32 ? 0.88 : 0.65;
     const int wgs = p.n_chunks * p.n_head_tiles;
     const double rounds = std::ceil((double)wgs / cu_count);
-    const double steps = std::ceil((double)p.chunk / p.block_tokens) + 1.0;
+    const double steps = std::ceil((double)p.chunk / p.block_tokens) + (paged ? 2.0 : 1.0);
     const double share = (p.n_head_tiles > 1 && !p.xcd_remap) ? 1.3 : 1.0;
     const double partial_bytes = (double)p.n_slots * num_heads * (kDV * p.part_bytes + 8);
     // the combine merges up to 128 slots of a tile per memory round trip
@@ -96,11 +96,11 @@ double modelled_us(const Plan &p, int num_heads, int batch, int cu_count)
 }  // namespace
 
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
-               int num_splits, int cu_count)
+               int num_splits, int cu_count, bool paged)
 {
     Plan p{};
     if (total_tokens <= 0) {
-        p.head_tile = fp32 ? 16 : (num_heads % 64 == 0) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
+        p.head_tile = fp32 ? 16 : (num_heads % 64 == 0 && !paged) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
         p.block_tokens = fp32 ? 16 : 32;
         p.n_head_tiles = num_heads / p.head_tile;
         p.chunk = p.block_tokens;
@@ -128,7 +128,7 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
     Plan best{};
     double best_us = 0.0;
     for (int ht : {64, 32, 16}) {
-        if (num_heads % ht != 0)
+        if (num_heads % ht != 0 || (paged && ht == 64))
             continue;
         Plan c{};
         c.head_tile = ht;
@@ -140,7 +140,7 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
             w_lo = w_hi = num_splits;
         for (int w = w_lo; w <= w_hi; ++w) {
             set_chunks(c, total_tokens, batch, w);
-            const double us = modelled_us(c, num_heads, batch, cu_count);
+            const double us = modelled_us(c, num_heads, batch, cu_count, paged);
             if (best_us == 0.0 || us < best_us) {
                 best = c;
                 best_us = us;
@@ -183,7 +183,8 @@ enum class Dtype { kF16, kBF16, kF32 };
 int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seqlens,
                void *out, void *workspace, size_t workspace_bytes, int batch,
                int num_heads, int total_tokens, int num_splits, unsigned flags,
-               void *stream, int phases = kPhaseSplit | kPhaseCombine)
+               void *stream, int phases = kPhaseSplit | kPhaseCombine,
+               const Paging *paging = nullptr)
 {
     const bool split = (phases & kPhaseSplit) != 0;
     const bool combine = (phases & kPhaseCombine) != 0;
@@ -193,7 +194,8 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
         (combine && !aligned16(out)))
         return MLA_STATUS_MISALIGNED;
     const bool fp32 = dt == Dtype::kF32;
-    const Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, current_cu_count());
+    const Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, current_cu_count(),
+                             paging != nullptr);
     if (workspace_bytes < partials_bytes(p, num_heads))
         return MLA_STATUS_WORKSPACE_TOO_SMALL;
 
@@ -207,6 +209,7 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
     pb.total_tokens = total_tokens;
     pb.scale_log2 = scale_log2();
     pb.bf16 = dt == Dtype::kBF16;
+    pb.paging = paging ? *paging : Paging{nullptr, 0, 0, 0};
     const Partials w = carve_partials(workspace, p, num_heads);
     hipStream_t s = static_cast<hipStream_t>(stream);
 
@@ -339,6 +342,56 @@ int mla_decode_split_batched_fp16(const void *query, const void *cache, const in
         cache = query;  // nothing is read from the cache
     return mla::run_decode(mla::Dtype::kF16, query, cache, cu_seqlens, out, workspace, workspace_bytes,
                            batch, num_heads, total_tokens, num_splits, 0u, stream);
+}
+
+size_t mla_decode_paged_workspace_size(int batch, int num_heads, int total_tokens, int num_splits)
+{
+    if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
+        return 0;
+    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, num_splits,
+                                       mla::current_cu_count(), true);
+    return mla::partials_bytes(p, num_heads);
+}
+
+namespace {
+
+int paged_decode(mla::Dtype dt, const void *query, const void *kv_cache, const int *block_table,
+                 const int *cu_seqlens, void *out, void *workspace, size_t workspace_bytes, int batch,
+                 int num_heads, int total_tokens, int page_size, int num_pages, int block_table_stride,
+                 int num_splits, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0 || !cu_seqlens || !block_table ||
+        page_size < 32 || page_size > (1 << 20) || (page_size & (page_size - 1)) != 0 || num_pages < 1 ||
+        block_table_stride < 1)
+        return MLA_STATUS_INVALID_VALUE;
+    if (total_tokens == 0 && !kv_cache)
+        kv_cache = query;  // nothing is read from the cache
+    mla::Paging pg{block_table, __builtin_ctz((unsigned)page_size), block_table_stride, num_pages};
+    return mla::run_decode(dt, query, kv_cache, cu_seqlens, out, workspace, workspace_bytes, batch,
+                           num_heads, total_tokens, num_splits, 0u, stream,
+                           mla::kPhaseSplit | mla::kPhaseCombine, &pg);
+}
+
+}  // namespace
+
+int mla_decode_paged_fp16(const void *query, const void *kv_cache, const int *block_table,
+                          const int *cu_seqlens, void *out, void *workspace, size_t workspace_bytes,
+                          int batch, int num_heads, int total_tokens, int page_size, int num_pages,
+                          int block_table_stride, int num_splits, void *stream)
+{
+    return paged_decode(mla::Dtype::kF16, query, kv_cache, block_table, cu_seqlens, out, workspace,
+                        workspace_bytes, batch, num_heads, total_tokens, page_size, num_pages,
+                        block_table_stride, num_splits, stream);
+}
+
+int mla_decode_paged_bf16(const void *query, const void *kv_cache, const int *block_table,
+                          const int *cu_seqlens, void *out, void *workspace, size_t workspace_bytes,
+                          int batch, int num_heads, int total_tokens, int page_size, int num_pages,
+                          int block_table_stride, int num_splits, void *stream)
+{
+    return paged_decode(mla::Dtype::kBF16, query, kv_cache, block_table, cu_seqlens, out, workspace,
+                        workspace_bytes, batch, num_heads, total_tokens, page_size, num_pages,
+                        block_table_stride, num_splits, stream);
 }
 
 int mla_decode_split_bf16(const void *query, const void *cache, void *out,

@@ -42,6 +42,16 @@ struct Partials {
     float *l;
 };
 
+// Paged KV cache: token l of sequence b is row (l mod 2^page_shift) of page
+// block_table[b * bt_stride + (l >> page_shift)] of a cache of num_pages
+// pages [2^page_shift][576]. block_table == nullptr: the packed layout.
+struct Paging {
+    const int *block_table;
+    int page_shift;
+    int bt_stride;
+    int num_pages;
+};
+
 struct Problem {
     const void *q;          // [batch][num_heads][576]
     const void *c;          // [total_tokens][576]
@@ -52,10 +62,13 @@ struct Problem {
     int total_tokens;
     float scale_log2;       // softmax scale * log2(e)
     bool bf16;              // 16-bit path: q, c, out (and the partial O) in bf16, not fp16
+    Paging paging;          // c is a paged cache when paging.block_table != nullptr
 };
 
+// paged: head tiles of 16 or 32 only (the paged kernel needs dedicated
+// feeder waves) and one extra block per piece in the cost model.
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
-               int num_splits, int cu_count);
+               int num_splits, int cu_count, bool paged = false);
 size_t partials_bytes(const Plan &p, int num_heads);
 Partials carve_partials(void *ws, const Plan &p, int num_heads);
 

@@ -148,7 +148,7 @@ __device__ __forceinline__ void global_to_lds16(const void *base, int off, const
                  : "=&s"(saved_m0) : "v"(off), "s"(base), "s"(l) : "memory");
 }
 
-template <int HT, bool kTr, typename E>
+template <int HT, bool kTr, typename E, bool kPaged>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void splitkv_fp16_kernel(const E *__restrict__ q,
                          const E *__restrict__ c,
@@ -157,9 +157,12 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                          float *__restrict__ m_part,
                          float *__restrict__ l_part,
                          int num_heads, int batch, int total_tokens, int chunk,
-                         int n_head_tiles, int xcd_remap, float scale_log2)
+                         int n_head_tiles, int xcd_remap, float scale_log2, Paging pg)
 {
     using T = F16Tile<HT>;
+    // paged caches are fed by dedicated feeder waves, which prefetch the
+    // page of the next block (the O waves of a 64-head tile do not)
+    static_assert(!(kPaged && T::kOFeeds), "paged cache needs a head tile of 16 or 32");
     using E8 = typename Vec<E>::v8;
     using E4 = typename Vec<E>::v4;
     __shared__ __attribute__((aligned(1024))) E s_ring[T::kRing * T::kSlot];
@@ -207,22 +210,27 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         }
         b_first = l;
     }
-    // Calls body(b, p_lo, p_hi) for every non-empty piece [p_lo, p_hi) of
-    // sequence b inside this chunk. Every wave walks the same pieces and,
-    // per piece, passes the same number of barriers (nblk + 5).
+    // Calls body(b, seq_lo, p_org, p_lo, p_hi) for every non-empty piece
+    // [p_lo, p_hi) of sequence b (whose first token is seq_lo) inside this
+    // chunk. Blocks of the piece start at p_org: p_lo itself, or, for a paged
+    // cache, p_lo rounded down to a multiple of 32 tokens of the sequence, so
+    // that no block straddles a page (tokens before p_lo are masked). Every
+    // wave walks the same pieces and, per piece, passes the same number of
+    // barriers (nblk + 5).
     auto for_each_piece = [&](auto &&body) {
         for (int b = b_first; b < nseq; ++b) {
             int seq_lo = 0, seq_hi = total_tokens;
             if (cu_seqlens) {
-                seq_lo = min(max(cu_seqlens[b], 0), total_tokens);
-                seq_hi = min(max(cu_seqlens[b + 1], seq_lo), total_tokens);
+                seq_lo = __builtin_amdgcn_readfirstlane(min(max(cu_seqlens[b], 0), total_tokens));
+                seq_hi = __builtin_amdgcn_readfirstlane(min(max(cu_seqlens[b + 1], seq_lo), total_tokens));
             }
             if (seq_lo >= hi)
                 break;
             const int p_lo = max(seq_lo, lo);
             const int p_hi = min(seq_hi, hi);
+            const int p_org = kPaged ? p_lo - ((p_lo - seq_lo) & (T::kBT - 1)) : p_lo;
             if (p_lo < p_hi)
-                body(b, p_lo, p_hi);
+                body(b, seq_lo, p_org, p_lo, p_hi);
         }
     };
 
@@ -249,12 +257,40 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         global_to_lds16(base, min(rrow, lim) * (kDK * 2) + 2 * (kDV + 8 * ((ln & 7) ^ rope_swizzle(rrow))),
                         s_ring + slot * T::kSlot + T::kRope + 512 * ru);
     };
+    // Global address of token t0 of sequence b (first token seq_lo), in two
+    // steps so that a paged cache's block-table read can be issued early:
+    // page_of reads the page id (0 for the packed layout), src_at forms the
+    // address. The rows of a block that starts at t0 follow it contiguously
+    // (same page).
+    auto page_of = [&](int b, int seq_lo, int t0) -> int {
+        if constexpr (kPaged) {
+            // clamped: inconsistent tables stay memory-safe (wrong, not faulting)
+            const int col = min((t0 - seq_lo) >> pg.page_shift, pg.bt_stride - 1);
+            // a scalar load: the index is wave-uniform, and a vector load
+            // here would be waited for with vmcnt, i.e. behind every
+            // global->LDS load in flight
+            const auto *bt = (const __attribute__((address_space(4))) int *)pg.block_table;
+            return bt[(size_t)b * pg.bt_stride + col];
+        } else {
+            return 0;
+        }
+    };
+    auto src_at = [&](int page, int seq_lo, int t0) -> const E * {
+        if constexpr (kPaged) {
+            page = min(max(page, 0), pg.num_pages - 1);
+            const int l = t0 - seq_lo;
+            return c + (((size_t)page << pg.page_shift) + (l & ((1 << pg.page_shift) - 1))) * kDK;
+        } else {
+            return c + (size_t)t0 * kDK;
+        }
+    };
+    auto token_src = [&](int b, int seq_lo, int t0) { return src_at(page_of(b, seq_lo, t0), seq_lo, t0); };
     // Prologue loads of a piece, issued by all 8 waves (wave w: C_N rows
     // 4w..4w+3 and, for w < 4, the rope rows 8w..8w+7 of each block): Q* of
     // the head tile into the top kQBlocks slots first, then blocks
     // 0..kPre-1. Each wave waits for its own loads; the barrier after this
     // (A) then publishes Q* and those blocks to every wave.
-    auto prologue_loads = [&](int b, int p_lo, int p_hi) {
+    auto prologue_loads = [&](int b, int seq_lo, int p_org, int p_hi) {
         const E *qb = q + ((size_t)b * num_heads + head0) * kDK;
 #pragma unroll
         for (int j = 0; j < T::kQBlocks; ++j) {
@@ -264,14 +300,19 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             if (wave < 4)
                 dma_rope(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, wave);
         }
+        int pages[T::kPre];  // all page reads first: one wait for them all
+#pragma unroll
+        for (int blk = 0; blk < T::kPre; ++blk)
+            pages[blk] = page_of(b, seq_lo, min(p_org + blk * T::kBT, p_hi - 1));
 #pragma unroll
         for (int blk = 0; blk < T::kPre; ++blk) {
-            const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
+            const int t0 = min(p_org + blk * T::kBT, p_hi - 1);
+            const E *src = src_at(pages[blk], seq_lo, t0);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                dma_row(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk, 4 * wave + r);
+                dma_row(src, p_hi - 1 - t0, blk, 4 * wave + r);
             if (wave < 4)
-                dma_rope(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk, wave);
+                dma_rope(src, p_hi - 1 - t0, blk, wave);
         }
         MLA_WAIT_VMCNT(0);
     };
@@ -302,11 +343,11 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                            : *(const E8 *)(slot + r * (kDK - kDV) + a_off[kk - 12]);
         };
 
-        for_each_piece([&](int b, int p_lo, int p_hi) {
+        for_each_piece([&](int b, int seq_lo, int p_org, int p_lo, int p_hi) {
             const int slot_out = split + b;
-            const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
+            const int nblk = (p_hi - p_org + T::kBT - 1) / T::kBT;
             lds_barrier();  // piece start: buffers are reused from the previous piece
-            prologue_loads(b, p_lo, p_hi);
+            prologue_loads(b, seq_lo, p_org, p_hi);
             lds_barrier();  // A: Q* and blocks 0..kPre-1 have landed
             // Q* fragments (B operand of S^T = C Q*^T): lane holds head
             // kSH*hg + 16*ns + l16 of the tile, dims 32*kk + 8*g .. +7. Q*
@@ -334,7 +375,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             for (int t = -1; t < nblk; ++t) {
                 if (t + 1 < nblk) {
                     const int blk = t + 1;
-                    const int t0 = p_lo + blk * T::kBT + 16 * th;
+                    const int t0 = p_org + blk * T::kBT + 16 * th;
                     const E *cslot = s_ring + (blk % T::kRing) * T::kSlot;
                     // ---- S^T tiles: tokens t0 + (0..15), heads of this wave.
                     // The 18 operand reads go out in batches of 3 K-steps,
@@ -381,7 +422,9 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         float mx = -INFINITY;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            sv[i] = (t0 + 4 * g + i) < p_hi ? st[i] * scale_log2 : -INFINITY;
+                            const int tok = t0 + 4 * g + i;
+                            const bool valid = kPaged ? (tok >= p_lo && tok < p_hi) : tok < p_hi;
+                            sv[i] = valid ? st[i] * scale_log2 : -INFINITY;
                             mx = fmaxf(mx, sv[i]);
                         }
                         mx = max_over_lane_groups(mx);
@@ -497,17 +540,18 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 }
             };
 
-            for_each_piece([&](int b, int p_lo, int p_hi) {
+            for_each_piece([&](int b, int seq_lo, int p_org, int p_lo, int p_hi) {
+                (void)p_lo;
                 const int slot_out = split + b;
-                const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
+                const int nblk = (p_hi - p_org + T::kBT - 1) / T::kBT;
                 // unit k of this wave's share of block blk; a block past the
                 // last re-reads the last token only
                 auto issue_unit = [&](int blk, int k) {
-                    const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
-                    load_unit(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk % T::kRing, k);
+                    const int t0 = min(p_org + blk * T::kBT, p_hi - 1);
+                    load_unit(token_src(b, seq_lo, t0), p_hi - 1 - t0, blk % T::kRing, k);
                 };
                 lds_barrier();  // piece start
-                prologue_loads(b, p_lo, p_hi);
+                prologue_loads(b, seq_lo, p_org, p_hi);
                 lds_barrier();  // A
                 lds_barrier();  // B
                 if constexpr (T::kOFeeds)
@@ -632,24 +676,39 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             });
         } else {
             // dedicated feeder waves (head tiles of 16 or 32 heads)
-            for_each_piece([&](int b, int p_lo, int p_hi) {
-                const int nblk = (p_hi - p_lo + T::kBT - 1) / T::kBT;
-                auto issue_unit = [&](int blk, int k) {
-                    const int t0 = min(p_lo + blk * T::kBT, p_hi - 1);
-                    load_unit(c + (size_t)t0 * kDK, p_hi - 1 - t0, blk % T::kRing, k);
+            for_each_piece([&](int b, int seq_lo, int p_org, int p_lo, int p_hi) {
+                (void)p_lo;
+                const int nblk = (p_hi - p_org + T::kBT - 1) / T::kBT;
+                // first token of block blk; a block past the last re-reads
+                // the last token only
+                auto t0_of = [&](int blk) { return min(p_org + blk * T::kBT, p_hi - 1); };
+                auto issue_block = [&](const E *src, int blk) {
+                    const int lim = p_hi - 1 - t0_of(blk);
+#pragma unroll
+                    for (int k = 0; k < T::kFeedUnits; ++k)
+                        load_unit(src, lim, blk % T::kRing, k);
                 };
                 lds_barrier();  // piece start
-                prologue_loads(b, p_lo, p_hi);
+                prologue_loads(b, seq_lo, p_org, p_hi);
+                // pages of blocks kPre..4, read before barrier B, and of each
+                // later block one step before it is issued, so that a paged
+                // cache's block-table reads arrive during a barrier
+                int rest[T::kRing - T::kPre];
+#pragma unroll
+                for (int blk = T::kPre; blk < T::kRing; ++blk)
+                    rest[blk - T::kPre] = page_of(b, seq_lo, t0_of(blk));
+                int next = page_of(b, seq_lo, t0_of(T::kRing));
                 lds_barrier();  // A
                 lds_barrier();  // B
-                feed_rest(issue_unit);
+#pragma unroll
+                for (int blk = T::kPre; blk < T::kRing; ++blk)
+                    issue_block(src_at(rest[blk - T::kPre], seq_lo, t0_of(blk)), blk);
                 for (int t = -1; t < nblk; ++t) {
                     // block t+4 into the slot of block t
                     const bool issue = t >= 0 && t + T::kRing < nblk;
                     if (issue) {
-#pragma unroll
-                        for (int k = 0; k < T::kFeedUnits; ++k)
-                            issue_unit(t + T::kRing, k);
+                        issue_block(src_at(next, seq_lo, t0_of(t + T::kRing)), t + T::kRing);
+                        next = page_of(b, seq_lo, t0_of(t + T::kRing + 1));
                     }
                     feed_wait(issue, t);
                     lds_barrier();
@@ -660,24 +719,31 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     }
 }
 
-template <int HT, bool kTr, typename E>
+template <int HT, bool kTr, typename E, bool kPaged>
 hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStream_t s)
 {
     const dim3 grid(p.n_chunks * p.n_head_tiles), block(F16Tile<HT>::kThreads);
-    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E>), grid, block, 0, s,
+    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged>), grid, block, 0, s,
                        (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens,
                        static_cast<E *>(w.o), w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
-                       p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2);
+                       p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2, pb.paging);
     return hipGetLastError();
 }
 
 template <typename E>
 hipError_t launch_e(const Problem &pb, const Plan &p, const Partials &w, bool tr_load, hipStream_t s)
 {
+    if (pb.paging.block_table) {  // the plan keeps paged caches to tiles of 16 or 32 heads
+        if (p.head_tile == 32)
+            return tr_load ? launch_ht<32, true, E, true>(pb, p, w, s) : launch_ht<32, false, E, true>(pb, p, w, s);
+        if (p.head_tile == 16)
+            return tr_load ? launch_ht<16, true, E, true>(pb, p, w, s) : launch_ht<16, false, E, true>(pb, p, w, s);
+        return hipErrorInvalidValue;
+    }
     switch (p.head_tile) {
-    case 64: return tr_load ? launch_ht<64, true, E>(pb, p, w, s) : launch_ht<64, false, E>(pb, p, w, s);
-    case 32: return tr_load ? launch_ht<32, true, E>(pb, p, w, s) : launch_ht<32, false, E>(pb, p, w, s);
-    default: return tr_load ? launch_ht<16, true, E>(pb, p, w, s) : launch_ht<16, false, E>(pb, p, w, s);
+    case 64: return tr_load ? launch_ht<64, true, E, false>(pb, p, w, s) : launch_ht<64, false, E, false>(pb, p, w, s);
+    case 32: return tr_load ? launch_ht<32, true, E, false>(pb, p, w, s) : launch_ht<32, false, E, false>(pb, p, w, s);
+    default: return tr_load ? launch_ht<16, true, E, false>(pb, p, w, s) : launch_ht<16, false, E, false>(pb, p, w, s);
     }
 }
 

@@ -45,6 +45,9 @@ WORKLOADS = {
     "batched": dict(kind="batched", n_h=128, batch=32,
                     desc="fp16 batched, B=32, N_b ~ U[512,16384] seed 42 (BASELINE config 5)"),
     "fp32": dict(kind="fp32", n_h=128, n=1024, desc="fp32 path, n_h=128, N=1024 (BASELINE config 1 shape on GPU)"),
+    "paged": dict(kind="paged", n_h=128, batch=32, page=64,
+                  desc="fp16 paged KV cache (64-token pages, shuffled), B=32, N_b ~ U[512,16384] seed 42 "
+                       "(config 5 through a block table)"),
     "bf16": dict(kind="bf16", n_h=128, n=4096, desc="bf16 KV cache, n_h=128, N=4096 (bf16 variant of config 2)"),
 }
 
@@ -180,7 +183,7 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(42)
 
-    if kind == "batched":
+    if kind in ("batched", "paged"):
         from ada_mla import synthetic
         seqlens = synthetic.batched_seqlens(wl["batch"], seed=42)
         batch = wl["batch"]
@@ -190,6 +193,18 @@ def main():
         cu_d = cu.to(dev)
         q_shape, c_shape = (batch, n_h, 576), (total, 576)
         dtype = torch.float16
+        if kind == "paged":
+            page = wl["page"]
+            need = [-(-int(n) // page) for n in seqlens]
+            n_pages = sum(need)
+            perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(42)).to(torch.int32)
+            bt = torch.zeros(batch, max(need), dtype=torch.int32)
+            k = 0
+            for b, nb in enumerate(need):
+                bt[b, :nb] = perm[k:k + nb]
+                k += nb
+            bt_d = bt.to(dev)
+            c_shape = (n_pages, page, 576)
     else:
         batch, total = 1, wl["n"]
         q_shape, c_shape = (n_h, 576), (total, 576)
@@ -199,7 +214,7 @@ def main():
     pool = max(2, math.ceil(args.flush_mb * 2**20 / pair_bytes))
     qs = [torch.randn(q_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
     cs = [torch.randn(c_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
-    out = torch.empty((batch, n_h, 512) if kind == "batched" else (n_h, 512), device=dev, dtype=dtype)
+    out = torch.empty((batch, n_h, 512) if kind in ("batched", "paged") else (n_h, 512), device=dev, dtype=dtype)
 
     splits = args.num_splits
     if kind in ("fp16", "bf16"):
@@ -207,6 +222,9 @@ def main():
         eff_splits = lib.mla_decode_split_num_splits(n_h, total, splits)
     elif kind == "fp32":
         ws_bytes = lib.mla_decode_fused_workspace_size(n_h, total, splits)
+        eff_splits = None
+    elif kind == "paged":
+        ws_bytes = lib.mla_decode_paged_workspace_size(batch, n_h, total, splits)
         eff_splits = None
     else:
         ws_bytes = lib.mla_decode_split_batched_workspace_size(batch, n_h, total, splits)
@@ -225,6 +243,10 @@ def main():
         elif kind == "bf16":
             check(lib.mla_decode_split_bf16(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
                                             n_h, total, splits, sptr), "bf16")
+        elif kind == "paged":
+            check(lib.mla_decode_paged_fp16(q.data_ptr(), c.data_ptr(), bt_d.data_ptr(), cu_d.data_ptr(),
+                                            out.data_ptr(), ws.data_ptr(), ws_bytes, batch, n_h, total, page,
+                                            c.shape[0], bt_d.shape[1], splits, sptr), "paged")
         elif kind == "fp32":
             check(lib.mla_decode_fused_fp32(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
                                             n_h, 576, total, splits, sptr), "fused_fp32")
@@ -307,7 +329,7 @@ def main():
         "roofline_time_us": max(bound_hbm, bound_mfma),
         "call_frac": max(bound_hbm, bound_mfma) / us_call,
     })
-    if kind in ("batched", "bf16"):
+    if kind in ("batched", "bf16", "paged"):
         roof["note"] = f"{kind} has no phase split: kernel_us is the whole call"
 
     res = {
@@ -326,7 +348,7 @@ def main():
         "config": {
             "workload": wl["desc"],
             "num_heads": n_h,
-            "seq_len": total if kind != "batched" else None,
+            "seq_len": total if kind not in ("batched", "paged") else None,
             "total_tokens": total,
             "batch": batch,
             "num_splits": eff_splits,

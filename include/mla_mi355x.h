@@ -151,6 +151,35 @@ int mla_decode_split_batched_bf16(const void *query, const void *cache,
                                   int batch, int num_heads, int total_tokens,
                                   int num_splits, void *stream);
 
+/* Paged KV cache (no reference counterpart: the reference reads one
+ * contiguous cache per call, csrc/mla_api.cpp:67-69). kv_cache is
+ * [num_pages x page_size x 576] (fp16 or bf16); token l of sequence b is row
+ * l % page_size of page block_table[b * block_table_stride + l / page_size]
+ * (int32 on the device). cu_seqlens [batch + 1] (int32, device) holds the
+ * prefix sums of the sequence lengths (cu_seqlens[0] = 0, cu_seqlens[batch]
+ * = total_tokens), query [batch x num_heads x 576], out
+ * [batch x num_heads x 512]; empty sequences give zero rows. page_size is a
+ * power of two >= 32. Page ids outside [0, num_pages) and block-table
+ * columns beyond block_table_stride are clamped (the result is then
+ * meaningless but every access stays inside the caller's buffers). The same
+ * split planner as the packed batched entry, with head tiles of 16 or 32. */
+size_t mla_decode_paged_workspace_size(int batch, int num_heads,
+                                       int total_tokens, int num_splits);
+int mla_decode_paged_fp16(const void *query, const void *kv_cache,
+                          const int *block_table, const int *cu_seqlens,
+                          void *out, void *workspace, size_t workspace_bytes,
+                          int batch, int num_heads, int total_tokens,
+                          int page_size, int num_pages,
+                          int block_table_stride, int num_splits,
+                          void *stream);
+int mla_decode_paged_bf16(const void *query, const void *kv_cache,
+                          const int *block_table, const int *cu_seqlens,
+                          void *out, void *workspace, size_t workspace_bytes,
+                          int batch, int num_heads, int total_tokens,
+                          int page_size, int num_pages,
+                          int block_table_stride, int num_splits,
+                          void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,10 @@ Contents, each restating a reference function:
 ``closed_form_batched``  the batched decode (no reference counterpart: the
                          reference has no batch dimension, csrc/mla_api.cpp:67-69)
                          = closed_form applied per sequence of a packed cache.
+``gather_paged`` /
+``closed_form_paged``    the paged-KV decode (no reference counterpart): the
+                         logical rows of every sequence gathered from the pages
+                         its block-table row names, then closed_form_batched.
 ``split_partials`` /
 ``lse_merge``            the split-KV partial results and the combine of
                          mla_decode_combine (csrc/mla_decode_splitk_fwd.cuh:894-939),
@@ -96,6 +100,28 @@ def closed_form_batched(q, c_packed, cu_seqlens, scale: float = SCALE,
         if hi > lo:
             out[b] = closed_form(q[b], c_packed[lo:hi], scale, dv)
     return out
+
+
+def gather_paged(kv_pages, block_table, cu_seqlens) -> np.ndarray:
+    """Packed cache [sum N_b, d] of a paged one: token l of sequence b is row
+    l % page_size of page block_table[b, l // page_size] of kv_pages
+    [num_pages, page_size, d]."""
+    kv = np.asarray(kv_pages)
+    bt = np.asarray(block_table, dtype=np.int64)
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    page = kv.shape[1]
+    rows = []
+    for b in range(bt.shape[0]):
+        n = int(cu[b + 1] - cu[b])
+        l = np.arange(n)
+        rows.append(kv[bt[b, l // page], l % page])
+    return np.concatenate(rows, axis=0) if rows else kv[:0, 0]
+
+
+def closed_form_paged(q, kv_pages, block_table, cu_seqlens, scale: float = SCALE,
+                      dv: int = HEAD_DIM_C) -> np.ndarray:
+    """closed_form_batched over the sequences of a paged cache."""
+    return closed_form_batched(q, gather_paged(kv_pages, block_table, cu_seqlens), cu_seqlens, scale, dv)
 
 
 def split_partials(q, c, bounds, scale: float = SCALE, dv: int = HEAD_DIM_C):

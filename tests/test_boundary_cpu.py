@@ -144,3 +144,47 @@ def test_batched_extension_rejects_bad_inputs():
         m.mla_decode_split_batched(q, c, torch.zeros(3, dtype=torch.int32))
     with pytest.raises(RuntimeError, match="both bfloat16"):
         m.mla_decode_split_batched(q.bfloat16(), c, torch.zeros(3, dtype=torch.int32))
+
+
+@pytest.mark.parametrize("fn", ["mla_decode_paged_fp16", "mla_decode_paged_bf16"])
+def test_paged_argument_errors(fn):
+    lib = capi.load()
+    f = getattr(lib, fn)
+    ok = dict(q=FAKE, kv=FAKE, bt=FAKE, cu=FAKE, out=FAKE, ws=FAKE, wsb=1 << 30, batch=4, nh=128, total=100,
+              page=64, pages=10, stride=4, splits=0)
+
+    def call(**kw):
+        a = {**ok, **kw}
+        return f(a["q"], a["kv"], a["bt"], a["cu"], a["out"], a["ws"], a["wsb"], a["batch"], a["nh"], a["total"],
+                 a["page"], a["pages"], a["stride"], a["splits"], None)
+    for bad in (dict(bt=None), dict(cu=None), dict(page=16), dict(page=96), dict(page=0), dict(pages=0),
+                dict(stride=0), dict(nh=24), dict(batch=0), dict(total=-1)):
+        assert call(**bad) == capi.STATUS_INVALID_VALUE, bad
+    assert call(kv=FAKE + 4) == capi.STATUS_MISALIGNED
+    assert call(wsb=16) == capi.STATUS_WORKSPACE_TOO_SMALL
+
+
+def test_paged_workspace_size():
+    lib = capi.load()
+    assert lib.mla_decode_paged_workspace_size(0, 128, 100, 0) == 0
+    assert lib.mla_decode_paged_workspace_size(4, 24, 100, 0) == 0
+    # one split: fp16 partial O for (1 chunk + 3 extra sequences) slots
+    assert lib.mla_decode_paged_workspace_size(4, 128, 100, 1) == 4 * 128 * 512 * 2 + 2 * 4 * 128 * 4
+
+
+def test_paged_extension_rejects_bad_inputs():
+    m = _ext()
+    q = torch.zeros(2, 128, 576, dtype=torch.float16)
+    kv = torch.zeros(4, 64, 576, dtype=torch.float16)
+    bt = torch.zeros(2, 3, dtype=torch.int32)
+    cu = torch.zeros(3, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="power of two"):
+        m.mla_decode_paged(q, torch.zeros(4, 48, 576, dtype=torch.float16), bt, cu)
+    with pytest.raises(RuntimeError, match="block_table must be"):
+        m.mla_decode_paged(q, kv, bt.long(), cu)
+    with pytest.raises(RuntimeError, match="batch rows"):
+        m.mla_decode_paged(q, kv, bt[:1], cu)
+    with pytest.raises(RuntimeError, match="kv_cache must both be float16 or both bfloat16"):
+        m.mla_decode_paged(q, kv.bfloat16(), bt, cu)
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        m.mla_decode_paged(q, kv, bt, cu)

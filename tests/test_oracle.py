@@ -214,3 +214,19 @@ def test_planted_restatement_divisor_is_caught(golden):
     c = case["c"].astype(np.float32)
     got = O.naive_cpu(q, c, divisor=math.sqrt(192), dv=576)
     assert not np.array_equal(got, case["ref_out"])
+
+
+def test_gather_paged_inverts_the_paged_layout():
+    # synthetic.paged_inputs scatters a packed cache into shuffled pages; the
+    # oracle's gather must return exactly the packed rows, and the paged
+    # closed form must equal the packed one
+    from ada_mla import synthetic
+    for page in (32, 64):
+        q, kv, bt, cu, c = synthetic.paged_inputs(16, [5, 0, 64, 65, 200, 1], page, seed=page)
+        assert np.array_equal(O.gather_paged(kv, bt, cu), c)
+        np.testing.assert_array_equal(O.closed_form_paged(q, kv, bt, cu), O.closed_form_batched(q, c, cu))
+    # a wrong page order is caught
+    q, kv, bt, cu, c = synthetic.paged_inputs(16, [100, 70], 32, seed=1)
+    bt2 = bt.copy()
+    bt2[0, [0, 1]] = bt2[0, [1, 0]]
+    assert not np.array_equal(O.gather_paged(kv, bt2, cu), c)
