@@ -22,18 +22,19 @@ STATUS_MISALIGNED = 2
 STATUS_WORKSPACE_TOO_SMALL = 3
 STATUS_HIP_ERROR = 4
 FLAG_SCALAR_TRANSPOSE = 1
+FLAG_FP32_PARTIALS = 4
 
 _vp, _i, _u, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint, ctypes.c_size_t
 _SIGNATURES = {
     "mla_abi_version": (_i, []),
     "mla_status_string": (ctypes.c_char_p, [_i]),
     "mla_last_hip_error": (_i, []),
-    "mla_decode_split_num_splits": (_i, [_i, _i, _i]),
+    "mla_decode_split_num_splits": (_i, [_i, _i, _i, _u]),
     "mla_decode_split_workspace_size": (_sz, [_i, _i, _i]),
     "mla_decode_split_fp16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "mla_decode_split_fp16_ex": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _u, _vp]),
     "mla_decode_split_fp16_partials": (_i, [_vp, _vp, _vp, _sz, _i, _i, _i, _u, _vp]),
-    "mla_decode_split_fp16_combine": (_i, [_vp, _sz, _vp, _i, _i, _i, _vp]),
+    "mla_decode_split_fp16_combine": (_i, [_vp, _sz, _vp, _i, _i, _i, _u, _vp]),
     "mla_decode_fused_workspace_size": (_sz, [_i, _i, _i]),
     "mla_decode_fused_fp32": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "mla_decode_split_batched_workspace_size": (_sz, [_i, _i, _i, _i]),

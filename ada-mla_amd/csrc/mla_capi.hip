@@ -71,15 +71,17 @@ void set_chunks(Plan &p, int total_tokens, int batch, int w)
     p.xcd_remap = (p.n_chunks % 8 == 0) ? 1 : 0;
 }
 
-// Modelled time of one fp16 decode call (us) for a plan, fitted to MI355X
-// measurements of this library: a fixed cost per call (two launches, the
-// prologue, the partial store), one 32-token step per block plus one, at a
-// step time that grows with the head tile (64: 1.5 us, 32: 0.88 us, 16:
-// 0.65 us with every CU busy), the partial traffic (written, then read by
-// the combine) at ~8 TB/s and the combine's memory round trips. Head tiles
-// that share a chunk but not an XCD re-read C from HBM, which the model
-// charges as slower steps.
-double modelled_us(const Plan &p, int num_heads, int batch, int cu_count, bool paged)
+// Modelled time of one 16-bit decode call (us) for a plan, fitted to MI355X
+// measurements of this library (forced plans over head tile, split count and
+// partial precision): a fixed cost per call (two launches, the prologue, the
+// partial store); the split kernel's block loop, one 32-token step per block
+// plus one at a step time that grows with the head tile (64: 1.5 us, 32:
+// 0.88 us, 16: 0.65 us with every CU busy), but no faster than streaming C
+// at ~6 TB/s; the partial round trip (written, then read by the combine)
+// at ~8 TB/s; and the combine's memory round trips. Head
+// tiles that share a chunk but not an XCD re-read C from HBM, which the
+// model charges as slower steps.
+double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, int cu_count, bool paged)
 {
     const double step_us = p.head_tile == 64 ? 1.5 : p.head_tile == 32 ? 0.88 : 0.65;
     const int wgs = p.n_chunks * p.n_head_tiles;
@@ -90,13 +92,14 @@ double modelled_us(const Plan &p, int num_heads, int batch, int cu_count, bool p
     // the combine merges up to 128 slots of a tile per memory round trip
     const double slots_per_seq = std::ceil((double)p.n_slots / batch);
     const double combine_trips = std::ceil(slots_per_seq / 128.0);
-    return 11.0 + rounds * steps * step_us * share + 2.0 * partial_bytes / 8.0e6 + 1.0 * combine_trips;
+    const double loop_us = std::max(rounds * steps * step_us * share, (double)total_tokens * kDK * 2 / 6.0e6);
+    return 11.0 + loop_us + 0.25e-6 * partial_bytes + 1.0 * combine_trips;
 }
 
 }  // namespace
 
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
-               int num_splits, int cu_count, bool paged)
+               int num_splits, int cu_count, bool paged, bool f32_partials)
 {
     Plan p{};
     if (total_tokens <= 0) {
@@ -107,7 +110,7 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
         p.n_chunks = 0;
         p.n_slots = batch;  // unused; keeps the workspace non-empty
         p.xcd_remap = 0;
-        p.part_bytes = fp32 ? 4 : 2;
+        p.part_bytes = (fp32 || f32_partials) ? 4 : 2;
         return p;
     }
     if (fp32) {
@@ -134,13 +137,13 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
         c.head_tile = ht;
         c.block_tokens = 32;
         c.n_head_tiles = num_heads / ht;
-        c.part_bytes = 2;
+        c.part_bytes = f32_partials ? 4 : 2;
         int w_lo = 1, w_hi = std::max(1, std::min(cu_count / c.n_head_tiles, ceil_div(total_tokens, c.block_tokens)));
         if (num_splits > 0)
             w_lo = w_hi = num_splits;
         for (int w = w_lo; w <= w_hi; ++w) {
             set_chunks(c, total_tokens, batch, w);
-            const double us = modelled_us(c, num_heads, batch, cu_count, paged);
+            const double us = modelled_us(c, num_heads, total_tokens, batch, cu_count, paged);
             if (best_us == 0.0 || us < best_us) {
                 best = c;
                 best_us = us;
@@ -171,6 +174,16 @@ Partials carve_partials(void *ws, const Plan &p, int num_heads)
 
 namespace {
 
+// Workspace of the 16-bit paths: enough for either partial precision (the
+// plans of the two may differ).
+size_t split_workspace_bytes(int num_heads, int total_tokens, int batch, int num_splits)
+{
+    const int cu = current_cu_count();
+    const Plan a = make_plan(false, num_heads, total_tokens, batch, num_splits, cu, false, false);
+    const Plan b = make_plan(false, num_heads, total_tokens, batch, num_splits, cu, false, true);
+    return std::max(partials_bytes(a, num_heads), partials_bytes(b, num_heads));
+}
+
 bool heads_ok(int num_heads) { return num_heads > 0 && num_heads % 16 == 0 && num_heads <= 4096; }
 
 constexpr int kPhaseSplit = 1;
@@ -194,8 +207,9 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
         (combine && !aligned16(out)))
         return MLA_STATUS_MISALIGNED;
     const bool fp32 = dt == Dtype::kF32;
+    const bool f32_part = !fp32 && !paging && (flags & MLA_FLAG_FP32_PARTIALS) != 0;
     const Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, current_cu_count(),
-                             paging != nullptr);
+                             paging != nullptr, f32_part);
     if (workspace_bytes < partials_bytes(p, num_heads))
         return MLA_STATUS_WORKSPACE_TOO_SMALL;
 
@@ -209,6 +223,7 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
     pb.total_tokens = total_tokens;
     pb.scale_log2 = scale_log2();
     pb.bf16 = dt == Dtype::kBF16;
+    pb.fp32 = fp32;
     pb.paging = paging ? *paging : Paging{nullptr, 0, 0, 0};
     const Partials w = carve_partials(workspace, p, num_heads);
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -248,19 +263,20 @@ const char *mla_status_string(int status)
 
 int mla_last_hip_error(void) { return mla::t_last_hip_error; }
 
-int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits)
+int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits, unsigned flags)
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count()).n_chunks;
+    return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(), false,
+                          (flags & MLA_FLAG_FP32_PARTIALS) != 0)
+        .n_chunks;
 }
 
 size_t mla_decode_split_workspace_size(int num_heads, int seq_length, int num_splits)
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    const mla::Plan p = mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count());
-    return mla::partials_bytes(p, num_heads);
+    return mla::split_workspace_bytes(num_heads, seq_length, 1, num_splits);
 }
 
 int mla_decode_split_fp16_ex(const void *query, const void *cache, void *out,
@@ -293,12 +309,13 @@ int mla_decode_split_fp16_partials(const void *query, const void *cache, void *w
 }
 
 int mla_decode_split_fp16_combine(const void *workspace, size_t workspace_bytes, void *out,
-                                  int num_heads, int seq_length, int num_splits, void *stream)
+                                  int num_heads, int seq_length, int num_splits, unsigned flags,
+                                  void *stream)
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return MLA_STATUS_INVALID_VALUE;
     return mla::run_decode(mla::Dtype::kF16, nullptr, nullptr, nullptr, out, const_cast<void *>(workspace),
-                           workspace_bytes, 1, num_heads, seq_length, num_splits, 0u, stream,
+                           workspace_bytes, 1, num_heads, seq_length, num_splits, flags, stream,
                            mla::kPhaseCombine);
 }
 
@@ -326,9 +343,7 @@ size_t mla_decode_split_batched_workspace_size(int batch, int num_heads, int tot
 {
     if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
         return 0;
-    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, num_splits,
-                                       mla::current_cu_count());
-    return mla::partials_bytes(p, num_heads);
+    return mla::split_workspace_bytes(num_heads, total_tokens, batch, num_splits);
 }
 
 int mla_decode_split_batched_fp16(const void *query, const void *cache, const int *cu_seqlens,

@@ -50,9 +50,10 @@ __device__ __forceinline__ floatx4 to_f32(const bf16x4 &v)
     return floatx4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
 }
 
-// PartT is the partials' type and the output's: fp16, bf16 (normalised
-// partials) or fp32 (unnormalised).
-template <typename PartT, int W>
+// PartT: the partials' type; OutT: the output's. On the 16-bit paths
+// (OutT fp16 / bf16) the partials are normalised by their sums and stored in
+// OutT or fp32; on the fp32 path they are unnormalised fp32.
+template <typename PartT, typename OutT, int W>
 __global__ __launch_bounds__(64 * (W > 8 ? W : 8))
 void combine_kernel(const PartT *__restrict__ o_part,
                     const float *__restrict__ m_part,
@@ -63,7 +64,7 @@ void combine_kernel(const PartT *__restrict__ o_part,
 {
     constexpr int kWaves = W > 8 ? W : 8;
     constexpr int kItems = kWaves / W;
-    constexpr bool kNorm = sizeof(PartT) == 2;  // fp16 partials are normalised by l
+    constexpr bool kNorm = !std::is_same<OutT, float>::value;
     using Batch = SlotBatch<PartT>;
     using V = typename Batch::V;
     __shared__ float s_m[W > 1 ? kWaves : 1][64];
@@ -179,36 +180,36 @@ void combine_kernel(const PartT *__restrict__ o_part,
     if (valid && k == 0) {
         const floatx4 t = (m != -INFINITY) ? acc * (1.0f / l) : floatx4{0.f, 0.f, 0.f, 0.f};
         const size_t o_off = ((size_t)b * num_heads + head) * kDV + dim0;
-        if constexpr (sizeof(PartT) == 4) {
+        if constexpr (std::is_same<OutT, float>::value) {
             *(floatx4 *)((float *)out + o_off) = t;
         } else {
-            using V = typename Batch::V;
-            const V h = {(PartT)t[0], (PartT)t[1], (PartT)t[2], (PartT)t[3]};
-            *(V *)((PartT *)out + o_off) = h;
+            using V = typename SlotBatch<OutT>::V;
+            const V h = {(OutT)t[0], (OutT)t[1], (OutT)t[2], (OutT)t[3]};
+            *(V *)((OutT *)out + o_off) = h;
         }
     }
 }
 
-template <typename PartT, int W>
+template <typename PartT, typename OutT, int W>
 void launch_w(const Problem &pb, const Plan &p, const Partials &w, int n_items, hipStream_t s)
 {
     constexpr int kWaves = W > 8 ? W : 8;
     constexpr int kItems = kWaves / W;
-    hipLaunchKernelGGL((combine_kernel<PartT, W>), dim3((n_items + kItems - 1) / kItems),
+    hipLaunchKernelGGL((combine_kernel<PartT, OutT, W>), dim3((n_items + kItems - 1) / kItems),
                        dim3(64 * kWaves), 0, s, static_cast<const PartT *>(w.o), w.m, w.l,
                        pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk, n_items);
 }
 
-template <typename PartT>
+template <typename PartT, typename OutT>
 void launch_part(const Problem &pb, const Plan &p, const Partials &w, int waves, int n_items,
                  hipStream_t s)
 {
     switch (waves) {
-    case 1: launch_w<PartT, 1>(pb, p, w, n_items, s); break;
-    case 2: launch_w<PartT, 2>(pb, p, w, n_items, s); break;
-    case 4: launch_w<PartT, 4>(pb, p, w, n_items, s); break;
-    case 8: launch_w<PartT, 8>(pb, p, w, n_items, s); break;
-    default: launch_w<PartT, 16>(pb, p, w, n_items, s); break;
+    case 1: launch_w<PartT, OutT, 1>(pb, p, w, n_items, s); break;
+    case 2: launch_w<PartT, OutT, 2>(pb, p, w, n_items, s); break;
+    case 4: launch_w<PartT, OutT, 4>(pb, p, w, n_items, s); break;
+    case 8: launch_w<PartT, OutT, 8>(pb, p, w, n_items, s); break;
+    default: launch_w<PartT, OutT, 16>(pb, p, w, n_items, s); break;
     }
 }
 
@@ -230,12 +231,14 @@ hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
 {
     const int n_items = pb.num_heads / 16 * (kDV / 16) * pb.batch;
     const int waves = combine_waves_per_item(p, pb.batch);
-    if (p.part_bytes == 4)
-        launch_part<float>(pb, p, w, waves, n_items, s);
-    else if (pb.bf16)
-        launch_part<__bf16>(pb, p, w, waves, n_items, s);
+    if (pb.fp32)
+        launch_part<float, float>(pb, p, w, waves, n_items, s);
+    else if (p.part_bytes == 4)
+        pb.bf16 ? launch_part<float, __bf16>(pb, p, w, waves, n_items, s)
+                : launch_part<float, _Float16>(pb, p, w, waves, n_items, s);
     else
-        launch_part<_Float16>(pb, p, w, waves, n_items, s);
+        pb.bf16 ? launch_part<__bf16, __bf16>(pb, p, w, waves, n_items, s)
+                : launch_part<_Float16, _Float16>(pb, p, w, waves, n_items, s);
     return hipGetLastError();
 }
 

@@ -26,7 +26,8 @@ struct Plan {
     int n_chunks;      // splits over the packed tokens
     int n_slots;       // partial-result slots: n_chunks + batch - 1
     int xcd_remap;     // 1: the head tiles of one chunk share an XCD
-    int part_bytes;    // bytes per partial O element: 2 (fp16 path), 4 (fp32 path)
+    int part_bytes;    // bytes per partial O element: 2 (16-bit paths), 4 (fp32 path, or 16-bit
+                       // paths with fp32 partials)
 };
 
 // Partial results of the split kernels: O in n_slots blocks of
@@ -61,6 +62,7 @@ struct Problem {
     int num_heads;
     int total_tokens;
     float scale_log2;       // softmax scale * log2(e)
+    bool fp32;              // fp32 path (q, c, out fp32; unnormalised fp32 partials)
     bool bf16;              // 16-bit path: q, c, out (and the partial O) in bf16, not fp16
     Paging paging;          // c is a paged cache when paging.block_table != nullptr
 };
@@ -68,7 +70,7 @@ struct Problem {
 // paged: head tiles of 16 or 32 only (the paged kernel needs dedicated
 // feeder waves) and one extra block per piece in the cost model.
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
-               int num_splits, int cu_count, bool paged = false);
+               int num_splits, int cu_count, bool paged = false, bool f32_partials = false);
 size_t partials_bytes(const Plan &p, int num_heads);
 Partials carve_partials(void *ws, const Plan &p, int num_heads);
 

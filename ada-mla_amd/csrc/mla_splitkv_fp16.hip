@@ -148,12 +148,13 @@ __device__ __forceinline__ void global_to_lds16(const void *base, int off, const
                  : "=&s"(saved_m0) : "v"(off), "s"(base), "s"(l) : "memory");
 }
 
-template <int HT, bool kTr, typename E, bool kPaged>
+// kF32Part: the partial O is stored in fp32 (still normalised) instead of E.
+template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void splitkv_fp16_kernel(const E *__restrict__ q,
                          const E *__restrict__ c,
                          const int *__restrict__ cu_seqlens,
-                         E *__restrict__ o_part,
+                         void *__restrict__ o_part,
                          float *__restrict__ m_part,
                          float *__restrict__ l_part,
                          int num_heads, int batch, int total_tokens, int chunk,
@@ -658,8 +659,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 lds_barrier();  // epilogue barrier of the S waves
                 // ---- epilogue: O of this piece normalised by its running sum
                 // (the halves' sums moved onto the reference max, exactly as
-                // the S waves compute the l they store), in fp16, tile by tile
-                E *obase = o_part + (size_t)slot_out * num_heads * kDV + lane * 4;
+                // the S waves compute the l they store), tile by tile
+                const size_t obase = (size_t)slot_out * num_heads * kDV + lane * 4;
 #pragma unroll
                 for (int hs = 0; hs < T::kNHS; ++hs) {
                     const int h = 16 * hs + l16;
@@ -669,8 +670,13 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
 #pragma unroll
                     for (int dt = 0; dt < 8; ++dt) {
                         const floatx4 v = o[hs][dt] * inv;
-                        const E4 hv = {(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
-                        *(E4 *)(obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt)) = hv;
+                        const size_t off = obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt);
+                        if constexpr (kF32Part) {
+                            *(floatx4 *)((float *)o_part + off) = v;
+                        } else {
+                            const E4 hv = {(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
+                            *(E4 *)((E *)o_part + off) = hv;
+                        }
                     }
                 }
             });
@@ -719,13 +725,12 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     }
 }
 
-template <int HT, bool kTr, typename E, bool kPaged>
+template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part = false>
 hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStream_t s)
 {
     const dim3 grid(p.n_chunks * p.n_head_tiles), block(F16Tile<HT>::kThreads);
-    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged>), grid, block, 0, s,
-                       (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens,
-                       static_cast<E *>(w.o), w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
+    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part>), grid, block, 0, s,
+                       (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens, w.o, w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2, pb.paging);
     return hipGetLastError();
 }
@@ -733,12 +738,19 @@ hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStr
 template <typename E>
 hipError_t launch_e(const Problem &pb, const Plan &p, const Partials &w, bool tr_load, hipStream_t s)
 {
-    if (pb.paging.block_table) {  // the plan keeps paged caches to tiles of 16 or 32 heads
+    if (pb.paging.block_table) {  // the plan keeps paged caches to tiles of 16 or 32 heads, fp16 partials
         if (p.head_tile == 32)
             return tr_load ? launch_ht<32, true, E, true>(pb, p, w, s) : launch_ht<32, false, E, true>(pb, p, w, s);
         if (p.head_tile == 16)
             return tr_load ? launch_ht<16, true, E, true>(pb, p, w, s) : launch_ht<16, false, E, true>(pb, p, w, s);
         return hipErrorInvalidValue;
+    }
+    if (p.part_bytes == 4) {  // fp32 partials (packed layout only)
+        switch (p.head_tile) {
+        case 64: return tr_load ? launch_ht<64, true, E, false, true>(pb, p, w, s) : launch_ht<64, false, E, false, true>(pb, p, w, s);
+        case 32: return tr_load ? launch_ht<32, true, E, false, true>(pb, p, w, s) : launch_ht<32, false, E, false, true>(pb, p, w, s);
+        default: return tr_load ? launch_ht<16, true, E, false, true>(pb, p, w, s) : launch_ht<16, false, E, false, true>(pb, p, w, s);
+        }
     }
     switch (p.head_tile) {
     case 64: return tr_load ? launch_ht<64, true, E, false>(pb, p, w, s) : launch_ht<64, false, E, false>(pb, p, w, s);

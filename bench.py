@@ -137,9 +137,16 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2000)
+    ap.add_argument("--spinup-ms", type=float, default=300.0,
+                    help="untimed decode calls for at least this long before the warm-up steps, so that "
+                         "the GPU's clocks are at their steady state (a cold start reads up to 15%% slower)")
     ap.add_argument("--workload", default="n4096", choices=sorted(WORKLOADS))
     ap.add_argument("--num-splits", type=int, default=0)
+    ap.add_argument("--partials", choices=("auto", "fp16", "fp32"), default="auto",
+                    help="fp16 single-sequence workloads: precision of the split partials (auto: fp32 for "
+                         "n65536, whose BASELINE config names fp32 partials, else fp16); the other precision "
+                         "is timed too and reported as alt_partials")
     ap.add_argument("--flush-mb", type=int, default=1024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
@@ -219,7 +226,9 @@ def main():
     splits = args.num_splits
     if kind in ("fp16", "bf16"):
         ws_bytes = lib.mla_decode_split_workspace_size(n_h, total, splits)
-        eff_splits = lib.mla_decode_split_num_splits(n_h, total, splits)
+        eff_splits = lib.mla_decode_split_num_splits(
+            n_h, total, splits, capi.FLAG_FP32_PARTIALS if args.partials == "fp32" or
+            (args.partials == "auto" and args.workload == "n65536") else 0)
     elif kind == "fp32":
         ws_bytes = lib.mla_decode_fused_workspace_size(n_h, total, splits)
         eff_splits = None
@@ -235,11 +244,16 @@ def main():
         if st != 0:
             raise capi.MlaError(fn, st)
 
+    partials = args.partials
+    if partials == "auto":
+        partials = "fp32" if args.workload == "n65536" else "fp16"
+    pflags = [capi.FLAG_FP32_PARTIALS if partials == "fp32" else 0]
+
     def phase1(i):
         q, c = qs[i % pool], cs[i % pool]
         if kind == "fp16":
             check(lib.mla_decode_split_fp16_partials(q.data_ptr(), c.data_ptr(), ws.data_ptr(), ws_bytes,
-                                                     n_h, total, splits, 0, sptr), "partials")
+                                                     n_h, total, splits, pflags[0], sptr), "partials")
         elif kind == "bf16":
             check(lib.mla_decode_split_bf16(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
                                             n_h, total, splits, sptr), "bf16")
@@ -258,8 +272,14 @@ def main():
     def phase2():
         if kind == "fp16":
             check(lib.mla_decode_split_fp16_combine(ws.data_ptr(), ws_bytes, out.data_ptr(), n_h, total, splits,
-                                                    sptr), "combine")
+                                                    pflags[0], sptr), "combine")
 
+    t_end = time.perf_counter() + args.spinup_ms * 1e-3
+    while time.perf_counter() < t_end:
+        for i in range(50):
+            phase1(i)
+            phase2()
+        torch.cuda.synchronize()
     for i in range(args.warmup):
         phase1(i)
         phase2()
@@ -303,6 +323,23 @@ def main():
     torch.cuda.synchronize()
     k_pair_us = statistics.median(a.elapsed_time(b) * 1000.0 for a, b in zip(pa, pb))
 
+    # (4) fp16 single sequence: the same K calls with the other partial precision
+    alt = None
+    if kind == "fp16":
+        pflags[0] ^= capi.FLAG_FP32_PARTIALS
+        for i in range(args.warmup):
+            phase1(i)
+            phase2()
+        torch.cuda.synchronize()
+        start.record(stream)
+        for i in range(K):
+            phase1(args.warmup + i)
+            phase2()
+        end.record(stream)
+        torch.cuda.synchronize()
+        alt = {"partials": "fp16" if partials == "fp32" else "fp32", "us_per_call": start.elapsed_time(end) * 1000.0 / K}
+        pflags[0] ^= capi.FLAG_FP32_PARTIALS
+
     alg_bytes, alg_flops = algorithmic(kind, n_h, total, batch)
     achieved = alg_bytes / (k_us * 1e-6) / 1e9
     mfma_peak = MFMA_F32_PEAK_TFS if kind == "fp32" else MFMA_F16_PEAK_TFS
@@ -339,6 +376,7 @@ def main():
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
+        "spinup_ms": args.spinup_ms,
         "ms_per_step": total_ms / K,
         "higher_is_better": False,
         "scaling": "weak",
@@ -352,12 +390,15 @@ def main():
             "total_tokens": total,
             "batch": batch,
             "num_splits": eff_splits,
+            "partials": partials if kind == "fp16" else ("fp32" if kind == "fp32" else "fp16"),
             "cache_flush": f"{pool} distinct (Q*, C) buffers, {pool * pair_bytes / 2**20:.0f} MB, rotated per step",
             "parallelism": "single GPU",
         },
         "tbps": alg_bytes / (us_call * 1e-6) / 1e12,
         "roofline": roof,
     }
+    if alt is not None:
+        res["alt_partials"] = alt
     if not args.no_cpu:
         cn = 1024 if kind == "fp32" else (total if kind == "fp16" else 4096)
         res["cpu_baseline"] = cpu_baseline(n_h, cn)

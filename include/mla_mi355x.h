@@ -49,16 +49,24 @@ extern "C" {
  * second product with scalar LDS loads instead of the LDS transpose read. */
 #define MLA_FLAG_SCALAR_TRANSPOSE 1u
 
+/* mla_decode_split_fp16_ex / _partials / _combine: keep the split partials
+ * in fp32 instead of the input type (twice the partial traffic; the combine
+ * must be given the same flag as the split phase). The workspace size
+ * queries cover both precisions. */
+#define MLA_FLAG_FP32_PARTIALS 4u
+
 int mla_abi_version(void);
 const char *mla_status_string(int status);
 /* hipError_t of the last failed HIP call on this thread (0 if none). */
 int mla_last_hip_error(void);
 
-/* Number of splits (partial results per head) that mla_decode_split_fp16
- * uses for these arguments on the current device; 0 for invalid sizes.
+/* Number of splits (partial results per head) that mla_decode_split_fp16_ex
+ * uses for these arguments and flags on the current device; 0 for invalid
+ * sizes.
  * Replaces the fixed `num_splits = 4` of mla_decode_split
  * (csrc/mla_api.cpp:97). */
-int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits);
+int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits,
+                                unsigned flags);
 
 /* Workspace for mla_decode_split_fp16 (split partials: O normalised by its
  * running sum in fp16, running max and sum in fp32). Replaces the
@@ -100,7 +108,8 @@ int mla_decode_split_fp16_partials(const void *query, const void *cache,
 int mla_decode_split_fp16_combine(const void *workspace,
                                   size_t workspace_bytes, void *out,
                                   int num_heads, int seq_length,
-                                  int num_splits, void *stream);
+                                  int num_splits, unsigned flags,
+                                  void *stream);
 
 /* Workspace for mla_decode_fused_fp32. */
 size_t mla_decode_fused_workspace_size(int num_heads, int seq_length,

@@ -36,9 +36,9 @@ def test_abi_version_and_status_strings():
 
 def test_workspace_size_one_split():
     lib = capi.load()
-    # one split: 128 heads x 512 fp16 partial O + 2 x 128 fp32 (256-byte aligned);
-    # the fp32 path keeps fp32 partial O
-    assert lib.mla_decode_split_workspace_size(128, 4096, 1) == 128 * 512 * 2 + 2 * 512
+    # one split: 128 heads x 512 partial O + 2 x 128 fp32 (256-byte aligned); the
+    # 16-bit path's size covers fp32 partials (MLA_FLAG_FP32_PARTIALS) too
+    assert lib.mla_decode_split_workspace_size(128, 4096, 1) == 128 * 512 * 4 + 2 * 512
     assert lib.mla_decode_fused_workspace_size(16, 100, 1) == 16 * 512 * 4 + 2 * 256
 
 
@@ -58,7 +58,7 @@ def test_workspace_grows_with_splits_and_batch():
     assert b == 8 * (a - 2 * 4096) + 2 * 32768
     # batched: slots = splits + batch - 1
     s = lib.mla_decode_split_batched_workspace_size(32, 128, 270000, 64)
-    assert s == (64 + 31) * 128 * 512 * 2 + 2 * ((64 + 31) * 128 * 4)
+    assert s == (64 + 31) * 128 * 512 * 4 + 2 * ((64 + 31) * 128 * 4)
 
 
 def test_split_count_is_clamped_to_blocks():

@@ -297,3 +297,38 @@ def test_repeat_determinism():
     f = [capi.decode_fused_fp32(qt.float(), ct.float()) for _ in range(2)]
     torch.cuda.synchronize()
     assert torch.equal(f[0], f[1])
+
+
+# ------------------------------------------- fp32 partials (MLA_FLAG_FP32_PARTIALS)
+
+@pytest.mark.parametrize("n_h,n", [(16, 1), (16, 1000), (128, 33), (128, 4096), (48, 2500)])
+def test_fp32_partials(n_h, n):
+    print(f"fp32 partials n_h={n_h} N={n}", flush=True)
+    q, c = synthetic.decode_inputs(n_h, n, seed=400 + n)
+    got = _fp16(q, c, flags=capi.FLAG_FP32_PARTIALS)
+    _check16(got, O.closed_form(q, c), f"n_h={n_h} N={n}")
+    # the partial precision only moves the output by fp16-partial rounding
+    assert np.abs(got - _fp16(q, c)).max() < 2e-3
+
+
+def test_config3_n65536_fp32_partials():
+    # BASELINE config 3 names fp32 partials
+    q, c = synthetic.decode_inputs(128, 65536, seed=42)
+    _check16(_fp16(q, c, flags=capi.FLAG_FP32_PARTIALS), O.closed_form(q, c), "config 3, fp32 partials")
+
+
+@pytest.mark.parametrize("flags", [0, 4])
+def test_two_phase_api_equals_single_call(flags):
+    lib = capi.load()
+    q, c = synthetic.decode_inputs(128, 3000, seed=21)
+    qt, ct = _t(q), _t(c)
+    one = capi.decode_split_fp16(qt, ct, flags=flags)
+    out = torch.empty_like(one)
+    ws_bytes = lib.mla_decode_split_workspace_size(128, 3000, 0)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qt.device)
+    s = capi._stream(qt)
+    assert lib.mla_decode_split_fp16_partials(qt.data_ptr(), ct.data_ptr(), ws.data_ptr(), ws_bytes,
+                                              128, 3000, 0, flags, s) == 0
+    assert lib.mla_decode_split_fp16_combine(ws.data_ptr(), ws_bytes, out.data_ptr(), 128, 3000, 0, flags, s) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(one, out)
