@@ -98,8 +98,10 @@ double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, in
 
 }  // namespace
 
-Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
-               int num_splits, int cu_count, bool paged, bool f32_partials)
+namespace {
+
+Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
+                  int num_splits, int cu_count, bool paged, bool f32_partials)
 {
     Plan p{};
     if (total_tokens <= 0) {
@@ -152,6 +154,40 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
     }
     return best;
 }
+
+}  // namespace
+
+// compute_plan searches a few hundred candidate plans (a few us of host
+// time); decode loops repeat the same arguments, so each host thread keeps
+// its last few plans.
+Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
+               int num_splits, int cu_count, bool paged, bool f32_partials)
+{
+    struct Entry {
+        int key[8];
+        Plan plan;
+    };
+    constexpr int kEntries = 16;
+    thread_local Entry cache[kEntries];
+    thread_local int filled = 0, next = 0;
+    const int key[8] = {fp32, num_heads, total_tokens, batch, num_splits, cu_count, paged, f32_partials};
+    for (int e = 0; e < filled; ++e) {
+        bool hit = true;
+        for (int k = 0; k < 8; ++k)
+            hit = hit && cache[e].key[k] == key[k];
+        if (hit)
+            return cache[e].plan;
+    }
+    const Plan p = compute_plan(fp32, num_heads, total_tokens, batch, num_splits, cu_count, paged, f32_partials);
+    Entry &slot = cache[next];
+    for (int k = 0; k < 8; ++k)
+        slot.key[k] = key[k];
+    slot.plan = p;
+    next = (next + 1) % kEntries;
+    filled = filled < kEntries ? filled + 1 : kEntries;
+    return p;
+}
+
 
 size_t partials_bytes(const Plan &p, int num_heads)
 {

@@ -188,3 +188,15 @@ def test_paged_extension_rejects_bad_inputs():
         m.mla_decode_paged(q, kv.bfloat16(), bt, cu)
     with pytest.raises(RuntimeError, match="GPU tensors"):
         m.mla_decode_paged(q, kv, bt, cu)
+
+
+def test_plan_cache_returns_the_same_plans():
+    # plans are cached per host thread (16 entries): more distinct argument
+    # sets than entries, asked twice in different orders, give the same answers
+    lib = capi.load()
+    args = [(nh, n, s) for nh in (16, 32, 128) for n in (1, 100, 4096, 65536) for s in (0, 3, 64)]
+    first = {a: (lib.mla_decode_split_num_splits(*a, 0), lib.mla_decode_split_workspace_size(*a)) for a in args}
+    for a in reversed(args):
+        assert (lib.mla_decode_split_num_splits(*a, 0), lib.mla_decode_split_workspace_size(*a)) == first[a], a
+    # the flag is part of the key
+    assert lib.mla_decode_split_num_splits(128, 65536, 0, 0) != lib.mla_decode_split_num_splits(128, 65536, 0, 4)
