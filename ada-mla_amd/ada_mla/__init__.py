@@ -6,6 +6,8 @@ reference's ``ada_mla`` extension module (csrc/mla_api.cpp:115-120).
     out = ada_mla.mla_decode_fused(q, c)   # fp32 (the reference's --fp32 path)
     out = ada_mla.mla_decode_split_batched(q, c_packed, cu_seqlens)  # [B, n_h, 512]
     out = ada_mla.mla_decode_paged(q, kv_pages, block_table, cu_seqlens)  # paged KV cache
+    q = ada_mla.mla_absorb_query(q_nope, q_rope, w_uk)     # the projections around
+    y = ada_mla.mla_project_output(o_star, w_uv, w_o)      # the decode (MLA block)
 
 The functions live in the compiled extension ``ada_mla._C`` (built by
 ada-mla_amd/build.py), which calls the HIP library through its C ABI
@@ -17,10 +19,10 @@ from __future__ import annotations
 import importlib
 
 __all__ = ["mla_decode_split", "mla_decode_fused", "mla_decode_split_batched", "mla_decode_paged",
-           "HEAD_DIM_C", "HEAD_DIM_ROPE", "HEAD_DIM_K", "extension"]
+           "mla_absorb_query", "mla_project_output", "HEAD_DIM_C", "HEAD_DIM_ROPE", "HEAD_DIM_K", "extension"]
 
 _EXPORTS = {"mla_decode_split", "mla_decode_fused", "mla_decode_split_batched", "mla_decode_paged",
-            "HEAD_DIM_C", "HEAD_DIM_ROPE", "HEAD_DIM_K"}
+            "mla_absorb_query", "mla_project_output", "HEAD_DIM_C", "HEAD_DIM_ROPE", "HEAD_DIM_K"}
 
 
 def extension():

@@ -42,6 +42,11 @@ _SIGNATURES = {
     "mla_decode_split_bf16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "mla_decode_split_batched_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "mla_decode_paged_workspace_size": (_sz, [_i, _i, _i, _i]),
+    "mla_project_output_workspace_size": (_sz, [_i, _i]),
+    "mla_absorb_query_fp16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "mla_absorb_query_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "mla_project_output_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
+    "mla_project_output_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "mla_decode_paged_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "mla_decode_paged_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _i, _vp]),
 }
@@ -201,4 +206,46 @@ def decode_paged(q, kv_cache, block_table, cu_seqlens, total_tokens: int, num_sp
     _check(fn, getattr(lib, fn)(q.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), cu_seqlens.data_ptr(),
                                 out.data_ptr(), ws.data_ptr(), ws_bytes, b, n_h, total_tokens, page_size,
                                 num_pages, block_table.shape[1], num_splits, _stream(q)))
+    return out
+
+
+def _suffix(t):
+    import torch
+    return {torch.float16: "fp16", torch.bfloat16: "bf16"}[t.dtype]
+
+
+def absorb_query(q_nope, q_rope, w_uk, out=None):
+    """Q* [B, n_h, 576] = [q_nope W_UK[h], q_rope] (mla_absorb_query_*): q_nope [B, n_h, 128],
+    q_rope [B, n_h, 64], w_uk [n_h, 128, 512]."""
+    import torch
+    lib = load()
+    b, n_h = q_nope.shape[0], q_nope.shape[1]
+    assert q_nope.shape == (b, n_h, 128) and q_rope.shape == (b, n_h, 64) and w_uk.shape == (n_h, 128, 512)
+    assert q_rope.dtype == q_nope.dtype == w_uk.dtype
+    assert q_nope.is_contiguous() and q_rope.is_contiguous() and w_uk.is_contiguous()
+    if out is None:
+        out = torch.empty((b, n_h, HEAD_DIM_K), dtype=q_nope.dtype, device=q_nope.device)
+    fn = "mla_absorb_query_" + _suffix(q_nope)
+    _check(fn, getattr(lib, fn)(q_nope.data_ptr(), q_rope.data_ptr(), w_uk.data_ptr(), out.data_ptr(), b, n_h,
+                                _stream(q_nope)))
+    return out
+
+
+def project_output(o_star, w_uv, w_o, out=None):
+    """out [B, d_model] = concat_h(O*[:, h] W_UV[h]^T) W_O^T (mla_project_output_*): o_star
+    [B, n_h, 512], w_uv [n_h, 128, 512], w_o [d_model, n_h * 128]."""
+    import torch
+    lib = load()
+    b, n_h = o_star.shape[0], o_star.shape[1]
+    d_model = w_o.shape[0]
+    assert o_star.shape == (b, n_h, 512) and w_uv.shape == (n_h, 128, 512) and w_o.shape == (d_model, n_h * 128)
+    assert o_star.dtype == w_uv.dtype == w_o.dtype
+    assert o_star.is_contiguous() and w_uv.is_contiguous() and w_o.is_contiguous()
+    if out is None:
+        out = torch.empty((b, d_model), dtype=o_star.dtype, device=o_star.device)
+    ws_bytes = lib.mla_project_output_workspace_size(b, n_h)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=o_star.device)
+    fn = "mla_project_output_" + _suffix(o_star)
+    _check(fn, getattr(lib, fn)(o_star.data_ptr(), w_uv.data_ptr(), w_o.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                ws_bytes, b, n_h, d_model, _stream(o_star)))
     return out

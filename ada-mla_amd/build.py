@@ -26,7 +26,8 @@ BUILD = os.path.join(PKG_ROOT, "_build")
 INCLUDE = os.path.join(REPO, "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_SOURCES = ["mla_splitkv_fp16.hip", "mla_splitkv_fp32.hip", "mla_combine.hip", "mla_capi.hip"]
+HIP_SOURCES = ["mla_splitkv_fp16.hip", "mla_splitkv_fp32.hip", "mla_combine.hip", "mla_capi.hip",
+               "mla_block.hip"]
 LIB_NAME = "libmla_mi355x.so"
 
 HIPCC_FLAGS = [
@@ -63,7 +64,8 @@ def build_lib(jobs: int = 4) -> str:
                 print(out)
     lib = os.path.join(OUT_DIR, LIB_NAME)
     tmp = lib + ".tmp"
-    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp,
+          f"-L{os.path.join(ROCM, 'lib')}", "-lrocblas"])
     os.replace(tmp, lib)
     return lib
 

@@ -213,6 +213,68 @@ at::Tensor mla_decode_paged(const at::Tensor &query_in, const at::Tensor &kv_in,
     return out;
 }
 
+void check_16bit(const at::Tensor &t, at::ScalarType dt, const char *fn, const char *name)
+{
+    TORCH_CHECK(t.scalar_type() == dt, fn, ": ", name, " must have the query's dtype (float16 or bfloat16)");
+    TORCH_CHECK(t.is_cuda(), fn, ": ", name, " must be a GPU tensor");
+}
+
+// No reference code (the math is README.md:76-85): Q* = [q_nope W_UK[h], q_rope].
+at::Tensor mla_absorb_query(const at::Tensor &q_nope_in, const at::Tensor &q_rope_in, const at::Tensor &w_uk_in)
+{
+    const char *fn = "mla_absorb_query";
+    const auto dt = q_nope_in.scalar_type();
+    TORCH_CHECK(dt == at::kHalf || dt == at::kBFloat16, fn, ": q_nope must be float16 or bfloat16");
+    TORCH_CHECK(q_nope_in.dim() == 3 && q_nope_in.size(2) == 128 && q_nope_in.size(0) >= 1, fn,
+                ": q_nope must be [batch, num_heads, 128], got ", q_nope_in.sizes());
+    const int64_t b = q_nope_in.size(0), nh = q_nope_in.size(1);
+    TORCH_CHECK(q_rope_in.dim() == 3 && q_rope_in.size(0) == b && q_rope_in.size(1) == nh && q_rope_in.size(2) == 64,
+                fn, ": q_rope must be [batch, num_heads, 64], got ", q_rope_in.sizes());
+    TORCH_CHECK(w_uk_in.dim() == 3 && w_uk_in.size(0) == nh && w_uk_in.size(1) == 128 && w_uk_in.size(2) == 512, fn,
+                ": w_uk must be [num_heads, 128, 512], got ", w_uk_in.sizes());
+    check_16bit(q_nope_in, dt, fn, "q_nope");
+    check_16bit(q_rope_in, dt, fn, "q_rope");
+    check_16bit(w_uk_in, dt, fn, "w_uk");
+    const at::OptionalDeviceGuard guard(q_nope_in.device());
+    const at::Tensor qn = q_nope_in.contiguous(), qr = q_rope_in.contiguous(), w = w_uk_in.contiguous();
+    at::Tensor out = at::empty({b, nh, MLA_HEAD_DIM_K}, qn.options());
+    auto f = dt == at::kHalf ? mla_absorb_query_fp16 : mla_absorb_query_bf16;
+    check_status(f(qn.data_ptr(), qr.data_ptr(), w.data_ptr(), out.data_ptr(), static_cast<int>(b),
+                   static_cast<int>(nh), stream_of(qn)),
+                 fn);
+    return out;
+}
+
+// No reference code (README.md:84-85): out = concat_h(O*[:, h] W_UV[h]^T) W_O^T.
+at::Tensor mla_project_output(const at::Tensor &o_in, const at::Tensor &w_uv_in, const at::Tensor &w_o_in)
+{
+    const char *fn = "mla_project_output";
+    const auto dt = o_in.scalar_type();
+    TORCH_CHECK(dt == at::kHalf || dt == at::kBFloat16, fn, ": o_star must be float16 or bfloat16");
+    TORCH_CHECK(o_in.dim() == 3 && o_in.size(2) == MLA_HEAD_DIM_V && o_in.size(0) >= 1, fn,
+                ": o_star must be [batch, num_heads, 512], got ", o_in.sizes());
+    const int64_t b = o_in.size(0), nh = o_in.size(1);
+    TORCH_CHECK(w_uv_in.dim() == 3 && w_uv_in.size(0) == nh && w_uv_in.size(1) == 128 && w_uv_in.size(2) == 512, fn,
+                ": w_uv must be [num_heads, 128, 512], got ", w_uv_in.sizes());
+    TORCH_CHECK(w_o_in.dim() == 2 && w_o_in.size(1) == nh * 128 && w_o_in.size(0) >= 1, fn,
+                ": w_o must be [d_model, num_heads * 128], got ", w_o_in.sizes());
+    check_16bit(o_in, dt, fn, "o_star");
+    check_16bit(w_uv_in, dt, fn, "w_uv");
+    check_16bit(w_o_in, dt, fn, "w_o");
+    const at::OptionalDeviceGuard guard(o_in.device());
+    const at::Tensor o = o_in.contiguous(), wuv = w_uv_in.contiguous(), wo = w_o_in.contiguous();
+    const int64_t d_model = wo.size(0);
+    at::Tensor out = at::empty({b, d_model}, o.options());
+    const size_t ws_bytes = mla_project_output_workspace_size(static_cast<int>(b), static_cast<int>(nh));
+    TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
+    at::Tensor ws = workspace(ws_bytes, o);
+    auto f = dt == at::kHalf ? mla_project_output_fp16 : mla_project_output_bf16;
+    check_status(f(o.data_ptr(), wuv.data_ptr(), wo.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
+                   static_cast<int>(b), static_cast<int>(nh), static_cast<int>(d_model), stream_of(o)),
+                 fn);
+    return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
@@ -232,6 +294,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
           "block_table [B,max_pages] int32, cu_seqlens [B+1] int32)",
           pybind11::arg("query"), pybind11::arg("kv_cache"), pybind11::arg("block_table"),
           pybind11::arg("cu_seqlens"), pybind11::arg("total_tokens") = -1, pybind11::arg("num_splits") = 0);
+    m.def("mla_absorb_query", &mla_absorb_query,
+          "Q* [B,n_h,576] = [q_nope W_UK[h], q_rope] (q_nope [B,n_h,128], q_rope [B,n_h,64], w_uk [n_h,128,512])",
+          pybind11::arg("q_nope"), pybind11::arg("q_rope"), pybind11::arg("w_uk"));
+    m.def("mla_project_output", &mla_project_output,
+          "out [B,d_model] = concat_h(O*[:,h] W_UV[h]^T) W_O^T (o_star [B,n_h,512], w_uv [n_h,128,512], "
+          "w_o [d_model,n_h*128])",
+          pybind11::arg("o_star"), pybind11::arg("w_uv"), pybind11::arg("w_o"));
     m.attr("HEAD_DIM_C") = MLA_HEAD_DIM_V;
     m.attr("HEAD_DIM_ROPE") = MLA_HEAD_DIM_K - MLA_HEAD_DIM_V;
     m.attr("HEAD_DIM_K") = MLA_HEAD_DIM_K;

@@ -48,15 +48,23 @@ WORKLOADS = {
     "paged": dict(kind="paged", n_h=128, batch=32, page=64,
                   desc="fp16 paged KV cache (64-token pages, shuffled), B=32, N_b ~ U[512,16384] seed 42 "
                        "(config 5 through a block table)"),
+    "block": dict(kind="block", n_h=128, batch=32, d_model=5120,
+                  desc="fp16 MLA block decode step: query absorption (W_UK) + config-5 batched decode + value "
+                       "and output projections (W_UV, W_O; d_model 5120), B=32"),
     "bf16": dict(kind="bf16", n_h=128, n=4096, desc="bf16 KV cache, n_h=128, N=4096 (bf16 variant of config 2)"),
 }
 
 
-def algorithmic(kind, n_h, total_tokens, batch=1):
-    """Bytes and flops of one call: e*(n_h*576 + N*576 + n_h*512), 2*n_h*N*1088."""
+def algorithmic(kind, n_h, total_tokens, batch=1, d_model=0):
+    """Bytes and flops of one call: e*(n_h*576 + N*576 + n_h*512), 2*n_h*N*1088; for the block
+    step also the weights W_UK, W_UV [n_h,128,512], W_O [d_model, n_h*128], the query halves and
+    the output read or written once, and their GEMM flops."""
     e = 4 if kind == "fp32" else 2
     bytes_ = e * (batch * n_h * 576 + total_tokens * 576 + batch * n_h * 512)
     flops = 2 * n_h * total_tokens * (576 + 512)
+    if kind == "block":
+        bytes_ += e * (2 * n_h * 128 * 512 + d_model * n_h * 128 + batch * n_h * 192 + batch * d_model)
+        flops += 2 * batch * (2 * n_h * 128 * 512 + n_h * 128 * d_model)
     return bytes_, flops
 
 
@@ -190,7 +198,7 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(42)
 
-    if kind in ("batched", "paged"):
+    if kind in ("batched", "paged", "block"):
         from ada_mla import synthetic
         seqlens = synthetic.batched_seqlens(wl["batch"], seed=42)
         batch = wl["batch"]
@@ -212,6 +220,19 @@ def main():
                 k += nb
             bt_d = bt.to(dev)
             c_shape = (n_pages, page, 576)
+        if kind == "block":
+            d_model = wl["d_model"]
+            gw = torch.Generator(device=dev)
+            gw.manual_seed(7)
+            mk = lambda *shape, sc=1.0: (torch.randn(shape, generator=gw, device=dev) * sc).to(dtype)
+            q_nope, q_rope = mk(batch, n_h, 128), mk(batch, n_h, 64)
+            w_uk, w_uv = mk(n_h, 128, 512, sc=128 ** -0.5), mk(n_h, 128, 512, sc=512 ** -0.5)
+            w_o = mk(d_model, n_h * 128, sc=(n_h * 128) ** -0.5)
+            q_star = torch.empty(batch, n_h, 576, device=dev, dtype=dtype)
+            o_star = torch.empty(batch, n_h, 512, device=dev, dtype=dtype)
+            y = torch.empty(batch, d_model, device=dev, dtype=dtype)
+            pws_bytes = lib.mla_project_output_workspace_size(batch, n_h)
+            pws = torch.empty(pws_bytes, dtype=torch.uint8, device=dev)
     else:
         batch, total = 1, wl["n"]
         q_shape, c_shape = (n_h, 576), (total, 576)
@@ -221,7 +242,8 @@ def main():
     pool = max(2, math.ceil(args.flush_mb * 2**20 / pair_bytes))
     qs = [torch.randn(q_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
     cs = [torch.randn(c_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
-    out = torch.empty((batch, n_h, 512) if kind in ("batched", "paged") else (n_h, 512), device=dev, dtype=dtype)
+    out = torch.empty((batch, n_h, 512) if kind in ("batched", "paged", "block") else (n_h, 512), device=dev,
+                      dtype=dtype)
 
     splits = args.num_splits
     if kind in ("fp16", "bf16"):
@@ -234,6 +256,9 @@ def main():
         eff_splits = None
     elif kind == "paged":
         ws_bytes = lib.mla_decode_paged_workspace_size(batch, n_h, total, splits)
+        eff_splits = None
+    elif kind == "block":
+        ws_bytes = lib.mla_decode_split_batched_workspace_size(batch, n_h, total, splits)
         eff_splits = None
     else:
         ws_bytes = lib.mla_decode_split_batched_workspace_size(batch, n_h, total, splits)
@@ -257,6 +282,14 @@ def main():
         elif kind == "bf16":
             check(lib.mla_decode_split_bf16(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
                                             n_h, total, splits, sptr), "bf16")
+        elif kind == "block":
+            check(lib.mla_absorb_query_fp16(q_nope.data_ptr(), q_rope.data_ptr(), w_uk.data_ptr(),
+                                            q_star.data_ptr(), batch, n_h, sptr), "absorb")
+            check(lib.mla_decode_split_batched_fp16(q_star.data_ptr(), c.data_ptr(), cu_d.data_ptr(),
+                                                    o_star.data_ptr(), ws.data_ptr(), ws_bytes, batch, n_h, total,
+                                                    splits, sptr), "batched")
+            check(lib.mla_project_output_fp16(o_star.data_ptr(), w_uv.data_ptr(), w_o.data_ptr(), y.data_ptr(),
+                                              pws.data_ptr(), pws_bytes, batch, n_h, d_model, sptr), "project")
         elif kind == "paged":
             check(lib.mla_decode_paged_fp16(q.data_ptr(), c.data_ptr(), bt_d.data_ptr(), cu_d.data_ptr(),
                                             out.data_ptr(), ws.data_ptr(), ws_bytes, batch, n_h, total, page,
@@ -340,7 +373,7 @@ def main():
         alt = {"partials": "fp16" if partials == "fp32" else "fp32", "us_per_call": start.elapsed_time(end) * 1000.0 / K}
         pflags[0] ^= capi.FLAG_FP32_PARTIALS
 
-    alg_bytes, alg_flops = algorithmic(kind, n_h, total, batch)
+    alg_bytes, alg_flops = algorithmic(kind, n_h, total, batch, wl.get("d_model", 0))
     achieved = alg_bytes / (k_us * 1e-6) / 1e9
     mfma_peak = MFMA_F32_PEAK_TFS if kind == "fp32" else MFMA_F16_PEAK_TFS
     tflops = alg_flops / (k_us * 1e-6) / 1e12
@@ -356,7 +389,9 @@ def main():
     roof.update({
         "traffic": traffic,
         "traffic_source": traffic_src,
-        "kernel": "splitkv_fp32_kernel" if kind == "fp32" else "splitkv_fp16_kernel",
+        "kernel": ("splitkv_fp32_kernel" if kind == "fp32" else
+                   "absorb GEMM + splitkv_fp16_kernel + combine + projection GEMMs" if kind == "block" else
+                   "splitkv_fp16_kernel"),
         "kernel_us": k_us,
         "kernel_us_event_pair_median": k_pair_us,
         "algorithmic_bytes": alg_bytes,
@@ -366,7 +401,7 @@ def main():
         "roofline_time_us": max(bound_hbm, bound_mfma),
         "call_frac": max(bound_hbm, bound_mfma) / us_call,
     })
-    if kind in ("batched", "bf16", "paged"):
+    if kind in ("batched", "bf16", "paged", "block"):
         roof["note"] = f"{kind} has no phase split: kernel_us is the whole call"
 
     res = {
@@ -386,7 +421,7 @@ def main():
         "config": {
             "workload": wl["desc"],
             "num_heads": n_h,
-            "seq_len": total if kind not in ("batched", "paged") else None,
+            "seq_len": total if kind not in ("batched", "paged", "block") else None,
             "total_tokens": total,
             "batch": batch,
             "num_splits": eff_splits,

@@ -189,6 +189,39 @@ int mla_decode_paged_bf16(const void *query, const void *kv_cache,
                           int block_table_stride, int num_splits,
                           void *stream);
 
+/* The projections around the decode, completing an MLA attention block's
+ * decode step (no reference code: the math is README.md:76-85, 104-110).
+ * Weights in torch Linear layout: w_uk, w_uv [num_heads][128][512] (the key
+ * and value halves of the latent up-projection), w_o [d_model][num_heads*128].
+ *
+ * mla_absorb_query_*: q_nope [batch][num_heads][128], q_rope
+ *   [batch][num_heads][64] -> q_star [batch][num_heads][576] with
+ *   q_star[..., :512] = q_nope W_UK[h] and q_star[..., 512:] = q_rope, the
+ *   query of mla_decode_split_batched_* / mla_decode_paged_* (no softmax
+ *   scale: the decode applies it).
+ * mla_project_output_*: o_star [batch][num_heads][512] (the decode's output)
+ *   -> out [batch][d_model] = concat_h(o_star[:, h] W_UV[h]^T) W_O^T, with
+ *   the per-head values in a caller workspace of
+ *   mla_project_output_workspace_size(batch, num_heads) bytes.
+ * GEMMs run on rocBLAS (fp32 accumulation); the first call on a host thread
+ * and device creates a rocBLAS handle, which allocates rocBLAS's own
+ * workspace -- unlike the decode entry points, these may allocate once. */
+size_t mla_project_output_workspace_size(int batch, int num_heads);
+int mla_absorb_query_fp16(const void *q_nope, const void *q_rope,
+                          const void *w_uk, void *q_star, int batch,
+                          int num_heads, void *stream);
+int mla_absorb_query_bf16(const void *q_nope, const void *q_rope,
+                          const void *w_uk, void *q_star, int batch,
+                          int num_heads, void *stream);
+int mla_project_output_fp16(const void *o_star, const void *w_uv,
+                            const void *w_o, void *out, void *workspace,
+                            size_t workspace_bytes, int batch, int num_heads,
+                            int d_model, void *stream);
+int mla_project_output_bf16(const void *o_star, const void *w_uv,
+                            const void *w_o, void *out, void *workspace,
+                            size_t workspace_bytes, int batch, int num_heads,
+                            int d_model, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,14 @@ Contents, each restating a reference function:
 ``closed_form_paged``    the paged-KV decode (no reference counterpart): the
                          logical rows of every sequence gathered from the pages
                          its block-table row names, then closed_form_batched.
+``absorb_query`` /
+``project_output`` /
+``block_unabsorbed``     the projections around the decode (no reference code;
+                         the math is README.md:64-110): the absorbed query
+                         [q_nope W_UK[h], q_rope], the value and output
+                         projections, and the same attention computed without
+                         absorption (keys C_N W_UK[h]^T and values C_N W_UV[h]^T
+                         per head), which the absorbed path must equal.
 ``split_partials`` /
 ``lse_merge``            the split-KV partial results and the combine of
                          mla_decode_combine (csrc/mla_decode_splitk_fwd.cuh:894-939),
@@ -122,6 +130,51 @@ def closed_form_paged(q, kv_pages, block_table, cu_seqlens, scale: float = SCALE
                       dv: int = HEAD_DIM_C) -> np.ndarray:
     """closed_form_batched over the sequences of a paged cache."""
     return closed_form_batched(q, gather_paged(kv_pages, block_table, cu_seqlens), cu_seqlens, scale, dv)
+
+
+def absorb_query(q_nope, q_rope, w_uk) -> np.ndarray:
+    """Q* [B, n_h, 576]: Q*[b, h, :512] = q_nope[b, h] @ w_uk[h] (w_uk [n_h, 128, 512]),
+    Q*[b, h, 512:] = q_rope[b, h] -- q*_i = c^Q W^UQ_i (W^UK_i)^T of README.md:76-80
+    without the scale, which the decode applies."""
+    q_nope = np.asarray(q_nope, dtype=np.float64)
+    w_uk = np.asarray(w_uk, dtype=np.float64)
+    nope = np.einsum("bhk,hkd->bhd", q_nope, w_uk)
+    return np.concatenate([nope, np.asarray(q_rope, dtype=np.float64)], axis=2)
+
+
+def project_output(o_star, w_uv, w_o) -> np.ndarray:
+    """out [B, d_model] = concat_h(o_star[:, h] @ w_uv[h]^T) @ w_o^T (README.md:84-85)."""
+    o_star = np.asarray(o_star, dtype=np.float64)
+    o = np.einsum("bhd,hkd->bhk", o_star, np.asarray(w_uv, dtype=np.float64))
+    return o.reshape(o.shape[0], -1) @ np.asarray(w_o, dtype=np.float64).T
+
+
+def block_unabsorbed(q_nope, q_rope, c_packed, cu_seqlens, w_uk, w_uv, w_o,
+                     scale: float = SCALE) -> np.ndarray:
+    """The decode step of an MLA block without weight absorption: per head,
+    keys [C_N W_UK[h]^T, C_R] and values C_N W_UV[h]^T, softmax attention with
+    the query [q_nope, q_rope], then the output projection. Equal to
+    project_output(closed_form_batched(absorb_query(...)), ...) in exact
+    arithmetic (README.md:68-80)."""
+    q_nope = np.asarray(q_nope, dtype=np.float64)
+    q_rope = np.asarray(q_rope, dtype=np.float64)
+    c = np.asarray(c_packed, dtype=np.float64)
+    w_uk = np.asarray(w_uk, dtype=np.float64)
+    w_uv = np.asarray(w_uv, dtype=np.float64)
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    B, n_h = q_nope.shape[0], q_nope.shape[1]
+    o = np.zeros((B, n_h, w_uv.shape[1]))
+    for b in range(B):
+        cb = c[cu[b]:cu[b + 1]]
+        if cb.shape[0] == 0:
+            continue
+        for h in range(n_h):
+            k = np.concatenate([cb[:, :HEAD_DIM_C] @ w_uk[h].T, cb[:, HEAD_DIM_C:]], axis=1)
+            v = cb[:, :HEAD_DIM_C] @ w_uv[h].T
+            q = np.concatenate([q_nope[b, h], q_rope[b, h]])
+            p = _softmax_rows((q @ k.T)[None, :] * scale)[0]
+            o[b, h] = p @ v
+    return o.reshape(B, -1) @ np.asarray(w_o, dtype=np.float64).T
 
 
 def split_partials(q, c, bounds, scale: float = SCALE, dv: int = HEAD_DIM_C):

@@ -200,3 +200,37 @@ def test_plan_cache_returns_the_same_plans():
         assert (lib.mla_decode_split_num_splits(*a, 0), lib.mla_decode_split_workspace_size(*a)) == first[a], a
     # the flag is part of the key
     assert lib.mla_decode_split_num_splits(128, 65536, 0, 0) != lib.mla_decode_split_num_splits(128, 65536, 0, 4)
+
+
+def test_block_projection_argument_errors():
+    lib = capi.load()
+    for fn in ("mla_absorb_query_fp16", "mla_absorb_query_bf16"):
+        f = getattr(lib, fn)
+        assert f(None, FAKE, FAKE, FAKE, 1, 16, None) == capi.STATUS_INVALID_VALUE
+        assert f(FAKE, FAKE, FAKE, FAKE, 0, 16, None) == capi.STATUS_INVALID_VALUE
+        assert f(FAKE, FAKE + 2, FAKE, FAKE, 1, 16, None) == capi.STATUS_MISALIGNED
+    for fn in ("mla_project_output_fp16", "mla_project_output_bf16"):
+        f = getattr(lib, fn)
+        assert f(FAKE, FAKE, None, FAKE, FAKE, 1 << 20, 1, 16, 64, None) == capi.STATUS_INVALID_VALUE
+        assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, 1, 16, 0, None) == capi.STATUS_INVALID_VALUE
+        assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 16, 1, 16, 64, None) == capi.STATUS_WORKSPACE_TOO_SMALL
+    # per-head values of B x n_h x 128 in the input dtype, 256-byte aligned
+    assert lib.mla_project_output_workspace_size(3, 16) == (3 * 16 * 128 * 2 + 255) // 256 * 256
+    assert lib.mla_project_output_workspace_size(0, 16) == 0
+
+
+def test_block_extension_rejects_bad_inputs():
+    m = _ext()
+    h = torch.float16
+    with pytest.raises(RuntimeError, match="q_rope must be"):
+        m.mla_absorb_query(torch.zeros(2, 16, 128, dtype=h), torch.zeros(2, 16, 32, dtype=h),
+                           torch.zeros(16, 128, 512, dtype=h))
+    with pytest.raises(RuntimeError, match="w_uk must be"):
+        m.mla_absorb_query(torch.zeros(2, 16, 128, dtype=h), torch.zeros(2, 16, 64, dtype=h),
+                           torch.zeros(16, 512, 128, dtype=h))
+    with pytest.raises(RuntimeError, match="w_o must be"):
+        m.mla_project_output(torch.zeros(2, 16, 512, dtype=h), torch.zeros(16, 128, 512, dtype=h),
+                             torch.zeros(64, 100, dtype=h))
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        m.mla_project_output(torch.zeros(2, 16, 512, dtype=h), torch.zeros(16, 128, 512, dtype=h),
+                             torch.zeros(64, 16 * 128, dtype=h))

@@ -230,3 +230,27 @@ def test_gather_paged_inverts_the_paged_layout():
     bt2 = bt.copy()
     bt2[0, [0, 1]] = bt2[0, [1, 0]]
     assert not np.array_equal(O.gather_paged(kv, bt2, cu), c)
+
+
+def test_absorbed_block_equals_unabsorbed_attention():
+    # the absorption identity of README.md:68-80, in float64: the absorbed
+    # query against the latent cache, then the value and output projections,
+    # equals per-head attention with explicit keys and values
+    rng = np.random.default_rng(11)
+    B, n_h, d_model = 3, 4, 40
+    seqlens = np.array([7, 0, 30])
+    cu = np.concatenate([[0], np.cumsum(seqlens)])
+    c = rng.standard_normal((cu[-1], 576))
+    q_nope = rng.standard_normal((B, n_h, 128)) * 0.1
+    q_rope = rng.standard_normal((B, n_h, 64))
+    w_uk = rng.standard_normal((n_h, 128, 512)) * 0.05
+    w_uv = rng.standard_normal((n_h, 128, 512)) * 0.05
+    w_o = rng.standard_normal((d_model, n_h * 128)) * 0.05
+    qs = O.absorb_query(q_nope, q_rope, w_uk)
+    assert qs.shape == (B, n_h, 576)
+    got = O.project_output(O.closed_form_batched(qs, c, cu), w_uv, w_o)
+    want = O.block_unabsorbed(q_nope, q_rope, c, cu, w_uk, w_uv, w_o)
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-12)
+    # a transposed key projection is caught
+    bad = O.absorb_query(q_nope, q_rope, np.ascontiguousarray(w_uk[:, :, ::-1]))
+    assert not np.allclose(O.project_output(O.closed_form_batched(bad, c, cu), w_uv, w_o), want)
