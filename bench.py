@@ -155,6 +155,8 @@ def main():
                     help="fp16 single-sequence workloads: precision of the split partials (auto: fp32 for "
                          "n65536, whose BASELINE config names fp32 partials, else fp16); the other precision "
                          "is timed too and reported as alt_partials")
+    ap.add_argument("--no-alt", action="store_true",
+                    help="skip the timing with the other partial precision (profiling runs: one kernel variant)")
     ap.add_argument("--flush-mb", type=int, default=1024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
@@ -358,7 +360,7 @@ def main():
 
     # (4) fp16 single sequence: the same K calls with the other partial precision
     alt = None
-    if kind == "fp16":
+    if kind == "fp16" and not args.no_alt:
         pflags[0] ^= capi.FLAG_FP32_PARTIALS
         for i in range(args.warmup):
             phase1(i)
