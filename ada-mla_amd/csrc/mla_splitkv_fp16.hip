@@ -97,18 +97,23 @@ constexpr float kLazyRescale = 8.0f;
 // part (chunks 64..71) in a separate area at 32 KB + r * 128, so that a
 // global->LDS load unit (64 chunks) is exactly one C_N row or 8 rope rows.
 // Chunks are XOR-swizzled within a row:
-//  - C_N: chunk c of row r sits at c ^ row_swizzle(r). row_swizzle is a
-//    bijection on r mod 16, so the 16 rows read at one chunk by the first
-//    product land on 16 distinct 16-byte bank groups (rows are 1024 bytes,
-//    a multiple of the 256-byte bank period), and the transpose reads of
-//    rows {r..r+3, r+8..r+11} (swizzles {0,2,4,6} and {8,...,14} apart)
-//    cover 16 distinct groups too;
+//  - C_N: chunk c of row r sits at c ^ (r mod 16). Rows are 1024 bytes, a
+//    multiple of the LDS bank period, so only the swizzle spreads the reads.
+//    Measured on gfx950 (rocprofv3 SQ_LDS_BANK_CONFLICT on probe kernels of
+//    each access pattern): the first product's 16-byte row reads (lane
+//    16g + i: row i, logical chunk 4j + g) are conflict-free when bit 0 of
+//    the stored chunk varies with the row's low two bits, and the transpose
+//    reads are conflict-free when it is the same for all rows of one
+//    instruction. Both hold with this swizzle because the second product
+//    takes its K (token) order as 8g + {0,2,4,6} (first transpose read) and
+//    8g + {1,3,5,7} (second): each transpose read touches rows of one
+//    parity. P's columns follow the same token order (see the P write in the S waves).
 //  - rope: chunk 64 + c' of row r sits at c' ^ rope_swizzle(r); rows are
 //    128 bytes, so rows r and r+1 share a bank period and the swizzle
 //    (r / 2) mod 8 separates the 8 row pairs of 16 consecutive rows.
 __device__ __forceinline__ int row_swizzle(int row)
 {
-    return ((row >> 2) & 1) | ((row & 3) << 1) | (row & 8);
+    return row & 15;
 }
 
 __device__ __forceinline__ int rope_swizzle(int row)
@@ -445,7 +450,15 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         }
                         l_lane[ns] = l_lane[ns] * alpha + ps;
                         const int hrow = T::kSH * hg + 16 * ns + l16;
-                        *(E4 *)(s_p[blk & 1] + hrow * T::kPRow + 16 * th + 4 * g) = ph;
+                        // P columns in the O waves' K order: within each
+                        // 8-token group, column j holds token 2j (j < 4) or
+                        // 2(j - 4) + 1. This lane's tokens 4(g & 1) + i of
+                        // group g >> 1 land in columns (i, i + 2) -> base,
+                        // base + 1 and base + 4, base + 5.
+                        E *pw = s_p[blk & 1] + hrow * T::kPRow + 16 * th + 8 * (g >> 1) + 2 * (g & 1);
+                        using E2 = E __attribute__((ext_vector_type(2)));
+                        *(E2 *)pw = E2{ph[0], ph[2]};
+                        *(E2 *)(pw + 4) = E2{ph[1], ph[3]};
                         if (g == 0)
                             s_m[blk & 1][th][hrow] = mn;
                     }
@@ -522,19 +535,20 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             // C_N^T operand of dims 128*ow + 16*dt .. +15 from a ring slot
             auto load_av = [&](const E *cs, int dt) -> E8 {
                 if constexpr (kTr) {
-                    // lane (g, j): rows 8g + j/4 (+4), dims 128*ow + 16*dt + 4*(j%4) .. +3
-                    const int r0 = 8 * g + (l16 >> 2);
+                    // lane (g, j): K index 8g + j/4 (+4) is token row 8g + 2(j/4)
+                    // (+1), dims 128*ow + 16*dt + 4*(j%4) .. +3
+                    const int r0 = 8 * g + 2 * (l16 >> 2);
                     const int cl = 16 * ow + 2 * dt + ((l16 & 3) >> 1);
                     const int sub = 4 * (l16 & 1);
                     const E4 lo4 = lds_read_tr16<E>(cs + r0 * kDV + 8 * (cl ^ row_swizzle(r0)) + sub);
-                    const E4 hi4 = lds_read_tr16<E>(cs + (r0 + 4) * kDV + 8 * (cl ^ row_swizzle(r0 + 4)) + sub);
+                    const E4 hi4 = lds_read_tr16<E>(cs + (r0 + 1) * kDV + 8 * (cl ^ row_swizzle(r0 + 1)) + sub);
                     return E8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
                 } else {
                     E8 v;
                     const int col = 128 * ow + 16 * dt + l16;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        const int r = 8 * g + j;
+                        const int r = 8 * g + (j < 4 ? 2 * j : 2 * j - 7);  // K order 8g + {0,2,4,6,1,3,5,7}
                         v[j] = cs[r * kDV + 8 * ((col >> 3) ^ row_swizzle(r)) + (col & 7)];
                     }
                     return v;
