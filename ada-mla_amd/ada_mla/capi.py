@@ -43,6 +43,9 @@ _SIGNATURES = {
     "mla_decode_split_batched_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "mla_decode_paged_workspace_size": (_sz, [_i, _i, _i, _i]),
     "mla_project_output_workspace_size": (_sz, [_i, _i]),
+    "mla_decode_split_fp8_workspace_size": (_sz, [_i, _i, _i, _i]),
+    "mla_decode_split_fp8": (_i, [_vp, _vp, ctypes.c_float, _vp, _vp, _sz, _i, _i, _i, _vp]),
+    "mla_decode_split_batched_fp8": (_i, [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "mla_absorb_query_fp16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
     "mla_absorb_query_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
     "mla_project_output_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
@@ -248,4 +251,42 @@ def project_output(o_star, w_uv, w_o, out=None):
     fn = "mla_project_output_" + _suffix(o_star)
     _check(fn, getattr(lib, fn)(o_star.data_ptr(), w_uv.data_ptr(), w_o.data_ptr(), out.data_ptr(), ws.data_ptr(),
                                 ws_bytes, b, n_h, d_model, _stream(o_star)))
+    return out
+
+
+def decode_split_fp8(q, c_fp8, c_scale: float, num_splits: int = 0, out=None):
+    """fp8-cache decode (mla_decode_split_fp8): q [n_h, 576] fp16, c_fp8 [N, 576] torch.float8_e4m3fn
+    (or uint8 bytes) holding C / c_scale -> [n_h, 512] fp16."""
+    import torch
+    lib = load()
+    assert q.dtype == torch.float16 and c_fp8.element_size() == 1
+    assert q.is_contiguous() and c_fp8.is_contiguous() and q.shape[1] == HEAD_DIM_K and c_fp8.shape[1] == HEAD_DIM_K
+    n_h, n = q.shape[0], c_fp8.shape[0]
+    if out is None:
+        out = torch.empty((n_h, HEAD_DIM_V), dtype=torch.float16, device=q.device)
+    ws_bytes = lib.mla_decode_split_fp8_workspace_size(1, n_h, n, num_splits)
+    if ws_bytes == 0:
+        raise MlaError("mla_decode_split_fp8_workspace_size", STATUS_INVALID_VALUE)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    _check("mla_decode_split_fp8", lib.mla_decode_split_fp8(q.data_ptr(), c_fp8.data_ptr(), float(c_scale), out.data_ptr(),
+                                                            ws.data_ptr(), ws_bytes, n_h, n, num_splits, _stream(q)))
+    return out
+
+
+def decode_split_batched_fp8(q, c_fp8, c_scale: float, cu_seqlens, num_splits: int = 0, out=None):
+    """Batched fp8-cache decode (mla_decode_split_batched_fp8); shapes as decode_split_batched_fp16."""
+    import torch
+    lib = load()
+    assert q.dtype == torch.float16 and c_fp8.element_size() == 1 and cu_seqlens.dtype == torch.int32
+    b, n_h, total = q.shape[0], q.shape[1], c_fp8.shape[0]
+    if out is None:
+        out = torch.empty((b, n_h, HEAD_DIM_V), dtype=torch.float16, device=q.device)
+    ws_bytes = lib.mla_decode_split_fp8_workspace_size(b, n_h, total, num_splits)
+    if ws_bytes == 0:
+        raise MlaError("mla_decode_split_fp8_workspace_size", STATUS_INVALID_VALUE)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    _check("mla_decode_split_batched_fp8",
+           lib.mla_decode_split_batched_fp8(q.data_ptr(), c_fp8.data_ptr() if total else None, float(c_scale),
+                                            cu_seqlens.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes, b, n_h,
+                                            total, num_splits, _stream(q)))
     return out

@@ -227,13 +227,13 @@ constexpr int kPhaseCombine = 2;
 
 // Shared body of every entry point; `phases` selects the split kernel, the
 // combine, or both (in that order, on one stream).
-enum class Dtype { kF16, kBF16, kF32 };
+enum class Dtype { kF16, kBF16, kF32, kF8Cache };
 
 int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seqlens,
                void *out, void *workspace, size_t workspace_bytes, int batch,
                int num_heads, int total_tokens, int num_splits, unsigned flags,
                void *stream, int phases = kPhaseSplit | kPhaseCombine,
-               const Paging *paging = nullptr)
+               const Paging *paging = nullptr, float c_scale = 1.0f)
 {
     const bool split = (phases & kPhaseSplit) != 0;
     const bool combine = (phases & kPhaseCombine) != 0;
@@ -243,9 +243,10 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
         (combine && !aligned16(out)))
         return MLA_STATUS_MISALIGNED;
     const bool fp32 = dt == Dtype::kF32;
-    const bool f32_part = !fp32 && !paging && (flags & MLA_FLAG_FP32_PARTIALS) != 0;
+    const bool f32_part = !fp32 && !paging && dt != Dtype::kF8Cache && (flags & MLA_FLAG_FP32_PARTIALS) != 0;
+    // the paged and fp8-cache kernels take tiles of 16 or 32 heads (planned like paged)
     const Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, current_cu_count(),
-                             paging != nullptr, f32_part);
+                             paging != nullptr || dt == Dtype::kF8Cache, f32_part);
     if (workspace_bytes < partials_bytes(p, num_heads))
         return MLA_STATUS_WORKSPACE_TOO_SMALL;
 
@@ -257,7 +258,9 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
     pb.batch = batch;
     pb.num_heads = num_heads;
     pb.total_tokens = total_tokens;
-    pb.scale_log2 = scale_log2();
+    pb.fp8 = dt == Dtype::kF8Cache;
+    pb.out_scale = pb.fp8 ? c_scale : 1.0f;
+    pb.scale_log2 = scale_log2() * pb.out_scale;  // fp8: logits of the dequantised cache
     pb.bf16 = dt == Dtype::kBF16;
     pb.fp32 = fp32;
     pb.paging = paging ? *paging : Paging{nullptr, 0, 0, 0};
@@ -443,6 +446,40 @@ int mla_decode_paged_bf16(const void *query, const void *kv_cache, const int *bl
     return paged_decode(mla::Dtype::kBF16, query, kv_cache, block_table, cu_seqlens, out, workspace,
                         workspace_bytes, batch, num_heads, total_tokens, page_size, num_pages,
                         block_table_stride, num_splits, stream);
+}
+
+size_t mla_decode_split_fp8_workspace_size(int batch, int num_heads, int total_tokens, int num_splits)
+{
+    if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
+        return 0;
+    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, num_splits,
+                                       mla::current_cu_count(), true);
+    return mla::partials_bytes(p, num_heads);
+}
+
+int mla_decode_split_batched_fp8(const void *query, const void *cache_fp8, float cache_scale,
+                                 const int *cu_seqlens, void *out, void *workspace, size_t workspace_bytes,
+                                 int batch, int num_heads, int total_tokens, int num_splits, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0 || !cu_seqlens ||
+        !(cache_scale > 0.0f && cache_scale < INFINITY))
+        return MLA_STATUS_INVALID_VALUE;
+    if (total_tokens == 0 && !cache_fp8)
+        cache_fp8 = query;  // nothing is read from the cache
+    return mla::run_decode(mla::Dtype::kF8Cache, query, cache_fp8, cu_seqlens, out, workspace, workspace_bytes,
+                           batch, num_heads, total_tokens, num_splits, 0u, stream,
+                           mla::kPhaseSplit | mla::kPhaseCombine, nullptr, cache_scale);
+}
+
+int mla_decode_split_fp8(const void *query, const void *cache_fp8, float cache_scale, void *out,
+                         void *workspace, size_t workspace_bytes, int num_heads, int seq_length,
+                         int num_splits, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1 || !(cache_scale > 0.0f && cache_scale < INFINITY))
+        return MLA_STATUS_INVALID_VALUE;
+    return mla::run_decode(mla::Dtype::kF8Cache, query, cache_fp8, nullptr, out, workspace, workspace_bytes, 1,
+                           num_heads, seq_length, num_splits, 0u, stream, mla::kPhaseSplit | mla::kPhaseCombine,
+                           nullptr, cache_scale);
 }
 
 int mla_decode_split_bf16(const void *query, const void *cache, void *out,

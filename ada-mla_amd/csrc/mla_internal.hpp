@@ -65,6 +65,8 @@ struct Problem {
     bool fp32;              // fp32 path (q, c, out fp32; unnormalised fp32 partials)
     bool bf16;              // 16-bit path: q, c, out (and the partial O) in bf16, not fp16
     Paging paging;          // c is a paged cache when paging.block_table != nullptr
+    bool fp8;               // c is OCP fp8 (E4M3FN) with per-tensor scale c_scale (q, out fp16)
+    float out_scale;        // multiplies the normalised partial O (c_scale for fp8, else 1)
 };
 
 // paged: head tiles of 16 or 32 only (the paged kernel needs dedicated

@@ -154,7 +154,11 @@ __device__ __forceinline__ void global_to_lds16(const void *base, int off, const
 }
 
 // kF32Part: the partial O is stored in fp32 (still normalised) instead of E.
-template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part>
+// kF8: the cache C is OCP fp8 (E4M3FN) [tokens][576] bytes and c points to
+// it (E is then fp16 for Q*, the ring and P); the feeder waves dequantise it
+// into the fp16 ring, exactly (every E4M3 value is an fp16 value), and the
+// per-tensor cache scale is folded into scale_log2 and out_scale.
+template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part, bool kF8>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void splitkv_fp16_kernel(const E *__restrict__ q,
                          const E *__restrict__ c,
@@ -163,9 +167,12 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                          float *__restrict__ m_part,
                          float *__restrict__ l_part,
                          int num_heads, int batch, int total_tokens, int chunk,
-                         int n_head_tiles, int xcd_remap, float scale_log2, Paging pg)
+                         int n_head_tiles, int xcd_remap, float scale_log2, Paging pg,
+                         float out_scale)
 {
     using T = F16Tile<HT>;
+    static_assert(!(kF8 && (kPaged || T::kOFeeds || !__is_same(E, _Float16))),
+                  "fp8 cache: packed layout, fp16 ring, head tile of 16 or 32");
     // paged caches are fed by dedicated feeder waves, which prefetch the
     // page of the next block (the O waves of a 64-head tile do not)
     static_assert(!(kPaged && T::kOFeeds), "paged cache needs a head tile of 16 or 32");
@@ -291,6 +298,34 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         }
     };
     auto token_src = [&](int b, int seq_lo, int t0) { return src_at(page_of(b, seq_lo, t0), seq_lo, t0); };
+    // fp8 cache: a staged unit is 8 bytes per lane, loaded into registers
+    // and written to the ring as 8 fp16 values (16 bytes) -- the C_N part of
+    // row `row` of the block at token t0 (lane -> logical chunk lane), or the
+    // rope part of rows 8*ru .. 8*ru+7 (lane -> row 8*ru + lane/8, logical
+    // chunk lane % 8). Rows past `lim` re-read row `lim`, as the loads above.
+    const unsigned char *c8 = reinterpret_cast<const unsigned char *>(c);
+    auto f8_load_row = [&](int t0, int lim, int row) -> uint2 {
+        return *(const uint2 *)(c8 + (size_t)(t0 + min(row, lim)) * kDK + 8 * lane);
+    };
+    auto f8_load_rope = [&](int t0, int lim, int ru) -> uint2 {
+        const int rrow = 8 * ru + (lane >> 3);
+        return *(const uint2 *)(c8 + (size_t)(t0 + min(rrow, lim)) * kDK + kDV + 8 * (lane & 7));
+    };
+    auto f8_to_f16 = [](uint2 v) -> half8 {
+        const half2v a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v.x, 1.0f, false);
+        const half2v b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v.x, 1.0f, true);
+        const half2v d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v.y, 1.0f, false);
+        const half2v e = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v.y, 1.0f, true);
+        return half8{a[0], a[1], b[0], b[1], d[0], d[1], e[0], e[1]};
+    };
+    auto f8_store_row = [&](uint2 v, int slot, int row) {
+        *(half8 *)(s_ring + slot * T::kSlot + row * kDV + 8 * (lane ^ row_swizzle(row))) = f8_to_f16(v);
+    };
+    auto f8_store_rope = [&](uint2 v, int slot, int ru) {
+        const int rrow = 8 * ru + (lane >> 3);
+        *(half8 *)(s_ring + slot * T::kSlot + T::kRope + rrow * (kDK - kDV) + 8 * ((lane & 7) ^ rope_swizzle(rrow))) =
+            f8_to_f16(v);
+    };
     // Prologue loads of a piece, issued by all 8 waves (wave w: C_N rows
     // 4w..4w+3 and, for w < 4, the rope rows 8w..8w+7 of each block): Q* of
     // the head tile into the top kQBlocks slots first, then blocks
@@ -305,6 +340,29 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 dma_row(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, 4 * wave + r);
             if (wave < 4)
                 dma_rope(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, wave);
+        }
+        if constexpr (kF8) {
+            // all loads first (in flight with Q*), then convert and store
+            uint2 v[T::kPre][5];
+#pragma unroll
+            for (int blk = 0; blk < T::kPre; ++blk) {
+                const int t0 = min(p_org + blk * T::kBT, p_hi - 1);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    v[blk][r] = f8_load_row(t0, p_hi - 1 - t0, 4 * wave + r);
+                if (wave < 4)
+                    v[blk][4] = f8_load_rope(t0, p_hi - 1 - t0, wave);
+            }
+#pragma unroll
+            for (int blk = 0; blk < T::kPre; ++blk) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    f8_store_row(v[blk][r], blk, 4 * wave + r);
+                if (wave < 4)
+                    f8_store_rope(v[blk][4], blk, wave);
+            }
+            MLA_WAIT_VMCNT(0);
+            return;
         }
         int pages[T::kPre];  // all page reads first: one wait for them all
 #pragma unroll
@@ -680,7 +738,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     const int h = 16 * hs + l16;
                     const float ls = s_l[0][h] * fast_exp2(s_m[0][0][h] - m_ref[hs]) +
                                      s_l[1][h] * fast_exp2(s_m[0][1][h] - m_ref[hs]);
-                    const float inv = 1.0f / ls;
+                    const float inv = out_scale / ls;
 #pragma unroll
                     for (int dt = 0; dt < 8; ++dt) {
                         const floatx4 v = o[hs][dt] * inv;
@@ -710,6 +768,67 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 };
                 lds_barrier();  // piece start
                 prologue_loads(b, seq_lo, p_org, p_hi);
+                if constexpr (kF8) {
+                    // fp8 cache: this feeder's units of a block are staged in
+                    // registers two steps before they are converted and
+                    // written (block b in st[(b + 1) & 1]): step t writes
+                    // block t+4 (block 3 at step -1, after barrier B) and
+                    // stages block t+6. The steps in which both happen run in
+                    // a loop of their own, so that the loads in flight are the
+                    // same at each of its steps and the compiler's vmcnt waits
+                    // leave the next block's loads in flight; the last steps
+                    // of the piece (write only, or nothing) follow.
+                    uint2 st[2][T::kFeedUnits];
+                    auto f8_issue = [&](uint2(&buf)[T::kFeedUnits], int blk) {
+                        const int t0 = t0_of(blk), lim = p_hi - 1 - t0;
+#pragma unroll
+                        for (int k = 0; k < T::kFeedUnits; ++k)
+                            buf[k] = k < T::kFeedRows
+                                         ? f8_load_row(t0, lim, T::kFeedRows * feeder + k)
+                                         : f8_load_rope(t0, lim, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
+                    };
+                    auto f8_write = [&](const uint2(&buf)[T::kFeedUnits], int blk) {
+#pragma unroll
+                        for (int k = 0; k < T::kFeedUnits; ++k) {
+                            if (k < T::kFeedRows)
+                                f8_store_row(buf[k], blk % T::kRing, T::kFeedRows * feeder + k);
+                            else
+                                f8_store_rope(buf[k], blk % T::kRing, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
+                        }
+                    };
+                    static_assert(T::kPre == 3 && T::kRing == 4, "fp8 staging assumes one block after Q*");
+                    if (3 < nblk)
+                        f8_issue(st[0], 3);
+                    if (4 < nblk)
+                        f8_issue(st[1], 4);
+                    lds_barrier();  // A
+                    lds_barrier();  // B
+                    // step t: write block t+4 from st[(t + 1) & 1], then stage block t+6 there
+                    auto full_step = [&](int t, uint2(&buf)[T::kFeedUnits]) {
+                        f8_write(buf, t + T::kRing);
+                        f8_issue(buf, t + T::kRing + 2);
+                        lds_barrier();
+                    };
+                    auto tail_step = [&](int t, uint2(&buf)[T::kFeedUnits]) {
+                        if (t + T::kRing < nblk)
+                            f8_write(buf, t + T::kRing);
+                        if (t + T::kRing + 2 < nblk)
+                            f8_issue(buf, t + T::kRing + 2);
+                        lds_barrier();
+                    };
+                    int t = -1;
+                    for (; t + 1 + T::kRing + 2 < nblk; t += 2) {
+                        full_step(t, st[0]);
+                        full_step(t + 1, st[1]);
+                    }
+                    for (; t < nblk; t += 2) {
+                        tail_step(t, st[0]);
+                        if (t + 1 < nblk)
+                            tail_step(t + 1, st[1]);
+                    }
+                    lds_barrier();  // epilogue barrier of the S waves
+                    return;
+                }
                 // pages of blocks kPre..4, read before barrier B, and of each
                 // later block one step before it is issued, so that a paged
                 // cache's block-table reads arrive during a barrier
@@ -739,13 +858,13 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     }
 }
 
-template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part = false>
+template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part = false, bool kF8 = false>
 hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStream_t s)
 {
     const dim3 grid(p.n_chunks * p.n_head_tiles), block(F16Tile<HT>::kThreads);
-    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part>), grid, block, 0, s,
+    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part, kF8>), grid, block, 0, s,
                        (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens, w.o, w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
-                       p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2, pb.paging);
+                       p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2, pb.paging, pb.out_scale);
     return hipGetLastError();
 }
 
@@ -780,6 +899,15 @@ hipError_t launch_splitkv_fp16(const Problem &pb, const Plan &p, const Partials 
 {
     if (p.n_chunks == 0)
         return hipSuccess;
+    if (pb.fp8) {  // fp16 query, fp8 cache; the plan keeps tiles of 16 or 32 heads, fp16 partials
+        if (p.head_tile == 32)
+            return tr_load ? launch_ht<32, true, _Float16, false, false, true>(pb, p, w, s)
+                           : launch_ht<32, false, _Float16, false, false, true>(pb, p, w, s);
+        if (p.head_tile == 16)
+            return tr_load ? launch_ht<16, true, _Float16, false, false, true>(pb, p, w, s)
+                           : launch_ht<16, false, _Float16, false, false, true>(pb, p, w, s);
+        return hipErrorInvalidValue;
+    }
     return pb.bf16 ? launch_e<__bf16>(pb, p, w, tr_load, s) : launch_e<_Float16>(pb, p, w, tr_load, s);
 }
 

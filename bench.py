@@ -51,6 +51,10 @@ WORKLOADS = {
     "block": dict(kind="block", n_h=128, batch=32, d_model=5120,
                   desc="fp16 MLA block decode step: query absorption (W_UK) + config-5 batched decode + value "
                        "and output projections (W_UV, W_O; d_model 5120), B=32"),
+    "fp8": dict(kind="fp8", n_h=128, n=4096, desc="fp8 (E4M3FN, per-tensor scale) KV cache, fp16 query/output, "
+                                                 "n_h=128, N=4096 (fp8 variant of config 2)"),
+    "fp8_n65536": dict(kind="fp8", n_h=128, n=65536, desc="fp8 (E4M3FN, per-tensor scale) KV cache, fp16 "
+                                                          "query/output, n_h=128, N=65536 (fp8 variant of config 3)"),
     "bf16": dict(kind="bf16", n_h=128, n=4096, desc="bf16 KV cache, n_h=128, N=4096 (bf16 variant of config 2)"),
 }
 
@@ -60,7 +64,8 @@ def algorithmic(kind, n_h, total_tokens, batch=1, d_model=0):
     step also the weights W_UK, W_UV [n_h,128,512], W_O [d_model, n_h*128], the query halves and
     the output read or written once, and their GEMM flops."""
     e = 4 if kind == "fp32" else 2
-    bytes_ = e * (batch * n_h * 576 + total_tokens * 576 + batch * n_h * 512)
+    ec = 1 if kind == "fp8" else e  # cache bytes per value
+    bytes_ = e * (batch * n_h * 576 + batch * n_h * 512) + ec * total_tokens * 576
     flops = 2 * n_h * total_tokens * (576 + 512)
     if kind == "block":
         bytes_ += e * (2 * n_h * 128 * 512 + d_model * n_h * 128 + batch * n_h * 192 + batch * d_model)
@@ -239,11 +244,18 @@ def main():
         batch, total = 1, wl["n"]
         q_shape, c_shape = (n_h, 576), (total, 576)
         dtype = {"fp32": torch.float32, "bf16": torch.bfloat16}.get(kind, torch.float16)
+        if kind == "fp8":
+            c_dtype = torch.float8_e4m3fn
     esz = 4 if dtype == torch.float32 else 2
     pair_bytes = (math.prod(q_shape) + math.prod(c_shape)) * esz
     pool = max(2, math.ceil(args.flush_mb * 2**20 / pair_bytes))
+    if kind == "fp8":
+        pair_bytes = math.prod(q_shape) * esz + math.prod(c_shape)
+        pool = max(2, math.ceil(args.flush_mb * 2**20 / pair_bytes))
     qs = [torch.randn(q_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
-    cs = [torch.randn(c_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
+    cs = [torch.randn(c_shape, generator=gen, device=dev, dtype=dtype if kind != "fp8" else torch.float32).to(
+        c_dtype) if kind == "fp8" else torch.randn(c_shape, generator=gen, device=dev, dtype=dtype)
+        for _ in range(pool)]
     out = torch.empty((batch, n_h, 512) if kind in ("batched", "paged", "block") else (n_h, 512), device=dev,
                       dtype=dtype)
 
@@ -258,6 +270,9 @@ def main():
         eff_splits = None
     elif kind == "paged":
         ws_bytes = lib.mla_decode_paged_workspace_size(batch, n_h, total, splits)
+        eff_splits = None
+    elif kind == "fp8":
+        ws_bytes = lib.mla_decode_split_fp8_workspace_size(1, n_h, total, splits)
         eff_splits = None
     elif kind == "block":
         ws_bytes = lib.mla_decode_split_batched_workspace_size(batch, n_h, total, splits)
@@ -281,6 +296,9 @@ def main():
         if kind == "fp16":
             check(lib.mla_decode_split_fp16_partials(q.data_ptr(), c.data_ptr(), ws.data_ptr(), ws_bytes,
                                                      n_h, total, splits, pflags[0], sptr), "partials")
+        elif kind == "fp8":
+            check(lib.mla_decode_split_fp8(q.data_ptr(), c.data_ptr(), 1.0, out.data_ptr(), ws.data_ptr(), ws_bytes,
+                                           n_h, total, splits, sptr), "fp8")
         elif kind == "bf16":
             check(lib.mla_decode_split_bf16(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
                                             n_h, total, splits, sptr), "bf16")
@@ -403,7 +421,7 @@ def main():
         "roofline_time_us": max(bound_hbm, bound_mfma),
         "call_frac": max(bound_hbm, bound_mfma) / us_call,
     })
-    if kind in ("batched", "bf16", "paged", "block"):
+    if kind in ("batched", "bf16", "paged", "block", "fp8"):
         roof["note"] = f"{kind} has no phase split: kernel_us is the whole call"
 
     res = {
@@ -418,7 +436,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"fp32": "fp32", "bf16": "bf16"}.get(kind, "fp16"),
+        "dtype": {"fp32": "fp32", "bf16": "bf16", "fp8": "fp16 (fp8 E4M3FN cache)"}.get(kind, "fp16"),
         "data": "synthetic (N(0,1), torch generator seed 42, resident in HBM)",
         "config": {
             "workload": wl["desc"],

@@ -189,6 +189,28 @@ int mla_decode_paged_bf16(const void *query, const void *kv_cache,
                           int block_table_stride, int num_splits,
                           void *stream);
 
+/* fp8 KV cache (no reference counterpart: the reference lists it as future
+ * work, README.md:408): query [.. x num_heads x 576] fp16, cache
+ * [tokens x 576] OCP fp8 E4M3FN bytes holding C / cache_scale (a per-tensor
+ * scale > 0), out fp16. The decode reads the cache at one byte per value
+ * (half the HBM traffic of fp16) and dequantises it exactly into fp16 on the
+ * way into LDS; products and softmax as on the fp16 path. Workspace from
+ * mla_decode_split_fp8_workspace_size(batch, num_heads, total_tokens,
+ * num_splits) (batch = 1 for the single-sequence entry). cu_seqlens as for
+ * mla_decode_split_batched_fp16. */
+size_t mla_decode_split_fp8_workspace_size(int batch, int num_heads,
+                                           int total_tokens, int num_splits);
+int mla_decode_split_fp8(const void *query, const void *cache_fp8,
+                         float cache_scale, void *out, void *workspace,
+                         size_t workspace_bytes, int num_heads,
+                         int seq_length, int num_splits, void *stream);
+int mla_decode_split_batched_fp8(const void *query, const void *cache_fp8,
+                                 float cache_scale, const int *cu_seqlens,
+                                 void *out, void *workspace,
+                                 size_t workspace_bytes, int batch,
+                                 int num_heads, int total_tokens,
+                                 int num_splits, void *stream);
+
 /* The projections around the decode, completing an MLA attention block's
  * decode step (no reference code: the math is README.md:76-85, 104-110).
  * Weights in torch Linear layout: w_uk, w_uv [num_heads][128][512] (the key

@@ -234,3 +234,17 @@ def test_block_extension_rejects_bad_inputs():
     with pytest.raises(RuntimeError, match="GPU tensor"):
         m.mla_project_output(torch.zeros(2, 16, 512, dtype=h), torch.zeros(16, 128, 512, dtype=h),
                              torch.zeros(64, 16 * 128, dtype=h))
+
+
+def test_fp8_argument_errors():
+    lib = capi.load()
+    f = lib.mla_decode_split_fp8
+    for bad_scale in (0.0, -1.0, float("inf"), float("nan")):
+        assert f(FAKE, FAKE, bad_scale, FAKE, FAKE, 1 << 30, 128, 64, 0, None) == capi.STATUS_INVALID_VALUE
+    assert f(FAKE, FAKE, 1.0, FAKE, FAKE, 1 << 30, 24, 64, 0, None) == capi.STATUS_INVALID_VALUE
+    assert f(FAKE, FAKE + 8, 1.0, FAKE, FAKE, 1 << 30, 128, 64, 0, None) == capi.STATUS_MISALIGNED
+    assert f(FAKE, FAKE, 1.0, FAKE, FAKE, 16, 128, 64, 0, None) == capi.STATUS_WORKSPACE_TOO_SMALL
+    g = lib.mla_decode_split_batched_fp8
+    assert g(FAKE, FAKE, 1.0, None, FAKE, FAKE, 1 << 30, 4, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
+    assert lib.mla_decode_split_fp8_workspace_size(0, 128, 10, 0) == 0
+    assert lib.mla_decode_split_fp8_workspace_size(1, 128, 10, 0) > 0

@@ -1,0 +1,85 @@
+"""GPU parity of the fp8 KV-cache path (mla_decode_split_fp8 and
+mla_decode_split_batched_fp8): the cache is stored as OCP fp8 E4M3FN holding
+C / scale, the query and output are fp16. The oracle is the float64 closed
+form on the dequantised cache (fp8 value x scale) and the fp16 query; there is
+no reference fp8 path (README.md:408 lists it as future work).
+
+Tolerance as for fp16: atol = rtol = 1e-2 and mean relative error < 5e-3 --
+the dequantisation itself is exact (every E4M3 value is an fp16 value), so
+only the kernel's own rounding (fp16 P, fp16 partials and output) remains.
+"""
+import numpy as np
+import pytest
+import torch
+
+from ada_mla import capi, synthetic
+from oracle import mla_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _fp8_inputs(n_h, n, seed, scale):
+    q = synthetic.normal((n_h, 576), seed, np.float16)
+    c32 = synthetic.normal((n, 576), seed + 1, np.float32)
+    c8 = torch.from_numpy(c32 / np.float32(scale)).to(torch.float8_e4m3fn)
+    c_deq = c8.float().double().numpy() * scale
+    return q, c8, c_deq
+
+
+def _check(got, ref, what):
+    assert np.isfinite(got).all(), what
+    np.testing.assert_allclose(got, ref, atol=1e-2, rtol=1e-2, err_msg=what)
+    rel = np.abs(got - ref).mean() / max(np.abs(ref).mean(), 1e-30)
+    assert rel < 5e-3, f"{what}: mean relative error {rel:.3e}"
+
+
+@pytest.mark.parametrize("n_h", [16, 32, 128])
+@pytest.mark.parametrize("n", [1, 17, 33, 100, 1000, 4097])
+def test_fp8_shapes(n_h, n):
+    print(f"fp8 n_h={n_h} N={n}", flush=True)
+    q, c8, cd = _fp8_inputs(n_h, n, seed=500 + n, scale=0.25)
+    out = capi.decode_split_fp8(torch.from_numpy(q).cuda(), c8.cuda(), 0.25)
+    torch.cuda.synchronize()
+    _check(out.double().cpu().numpy(), O.closed_form(q, cd), f"n_h={n_h} N={n}")
+
+
+@pytest.mark.parametrize("n_h,n,scale", [(128, 4096, 1.0), (128, 65536, 0.03125), (16, 32768, 3.0)])
+def test_fp8_benchmark_shapes(n_h, n, scale):
+    print(f"fp8 config n_h={n_h} N={n} scale={scale}", flush=True)
+    q, c8, cd = _fp8_inputs(n_h, n, seed=42, scale=scale)
+    out = capi.decode_split_fp8(torch.from_numpy(q).cuda(), c8.cuda(), scale)
+    torch.cuda.synchronize()
+    _check(out.double().cpu().numpy(), O.closed_form(q, cd), f"n_h={n_h} N={n}")
+
+
+def test_fp8_split_invariance_and_single_token():
+    q, c8, cd = _fp8_inputs(32, 3000, seed=3, scale=0.5)
+    ref = O.closed_form(q, cd)
+    for s in (1, 3, 40):
+        out = capi.decode_split_fp8(torch.from_numpy(q).cuda(), c8.cuda(), 0.5, num_splits=s)
+        torch.cuda.synchronize()
+        _check(out.double().cpu().numpy(), ref, f"splits={s}")
+    q1, c1, cd1 = _fp8_inputs(16, 1, seed=4, scale=2.0)
+    out = capi.decode_split_fp8(torch.from_numpy(q1).cuda(), c1.cuda(), 2.0)
+    torch.cuda.synchronize()
+    # one token: the output is that token's dequantised C_N row, rounded to fp16
+    want = np.repeat(cd1[:, :512], 16, axis=0).astype(np.float16).astype(np.float64)
+    assert np.array_equal(out.double().cpu().numpy(), want)
+
+
+def test_fp8_batched_with_empty():
+    seqlens = np.array([5, 0, 17, 1, 300, 64, 0, 1000, 33])
+    q, _, cu = synthetic.batched_inputs(128, seqlens, seed=9)
+    c32 = synthetic.normal((int(cu[-1]), 576), 10, np.float32)
+    c8 = torch.from_numpy(c32 / np.float32(0.5)).to(torch.float8_e4m3fn)
+    cd = c8.float().double().numpy() * 0.5
+    out = capi.decode_split_batched_fp8(torch.from_numpy(q).cuda(), c8.cuda(), 0.5, torch.from_numpy(cu).cuda(),
+                                        num_splits=7)
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    ref = O.closed_form_batched(q, cd, cu)
+    for b in range(len(seqlens)):
+        if seqlens[b] == 0:
+            assert not got[b].any()
+        else:
+            _check(got[b], ref[b], f"seq {b}")
