@@ -17,7 +17,13 @@
 //  * bf16 query/cache are accepted by mla_decode_split, mla_decode_fused and
 //    mla_decode_split_batched (bf16 MFMAs; the reference lists bf16 as
 //    future work, README.md:405-408).
+//  * mla_decode_split and mla_decode_split_batched also take a float8_e4m3fn
+//    cache with a float16 query: the cache holds C / cache_scale (keyword
+//    cache_scale, default 1) and is read at one byte per value (fp8 is
+//    future work in the reference too, README.md:408).
 #include <torch/extension.h>
+
+#include <cmath>
 
 #include <c10/hip/HIPStream.h>
 
@@ -34,9 +40,21 @@ void check_status(int st, const char *fn)
 
 // Shape and dtype are checked before the device so that every argument error
 // is reported the same way whatever the tensors' device.
+bool is_fp8_cache(const at::Tensor &query, const at::Tensor &cache)
+{
+    return cache.scalar_type() == at::kFloat8_e4m3fn && query.scalar_type() == at::kHalf;
+}
+
+void check_cache_scale(double cache_scale, const char *fn)
+{
+    TORCH_CHECK(std::isfinite(cache_scale) && cache_scale > 0, fn, ": cache_scale must be finite and > 0, got ",
+                cache_scale);
+}
+
 void check_pair(const at::Tensor &query, const at::Tensor &cache, const char *fn)
 {
-    TORCH_CHECK(query.scalar_type() == cache.scalar_type(), fn, ": query and cache must have the same dtype");
+    TORCH_CHECK(query.scalar_type() == cache.scalar_type() || is_fp8_cache(query, cache), fn,
+                ": query and cache must have the same dtype (or a float16 query with a float8_e4m3fn cache)");
     TORCH_CHECK(query.scalar_type() == at::kHalf || query.scalar_type() == at::kBFloat16 ||
                     query.scalar_type() == at::kFloat,
                 fn, ": dtype must be float16, bfloat16 or float32, got ", query.scalar_type());
@@ -70,8 +88,11 @@ at::Tensor workspace(size_t bytes, const at::Tensor &like)
 
 // Single sequence, dispatch on dtype.
 at::Tensor decode_single(const at::Tensor &query_in, const at::Tensor &cache_in, int64_t num_splits,
-                         const char *fn)
+                         double cache_scale, const char *fn)
 {
+    const bool fp8 = is_fp8_cache(query_in, cache_in);
+    if (fp8)
+        check_cache_scale(cache_scale, fn);
     check_pair(query_in, cache_in, fn);
     const at::OptionalDeviceGuard guard(query_in.device());
     const at::Tensor query = query_in.contiguous();
@@ -81,7 +102,13 @@ at::Tensor decode_single(const at::Tensor &query_in, const at::Tensor &cache_in,
     const int splits = static_cast<int>(num_splits);
     at::Tensor out = at::empty({nh, MLA_HEAD_DIM_V}, query.options());
     int st;
-    if (query.scalar_type() != at::kFloat) {
+    if (fp8) {
+        const size_t ws_bytes = mla_decode_split_fp8_workspace_size(1, nh, n, splits);
+        TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
+        at::Tensor ws = workspace(ws_bytes, query);
+        st = mla_decode_split_fp8(query.data_ptr(), cache.data_ptr(), static_cast<float>(cache_scale),
+                                  out.data_ptr(), ws.data_ptr(), ws_bytes, nh, n, splits, stream_of(query));
+    } else if (query.scalar_type() != at::kFloat) {
         const size_t ws_bytes = mla_decode_split_workspace_size(nh, n, splits);
         TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
         at::Tensor ws = workspace(ws_bytes, query);
@@ -102,26 +129,32 @@ at::Tensor decode_single(const at::Tensor &query_in, const at::Tensor &cache_in,
 
 // Reference: mla_decode_split (csrc/mla_api.cpp:86-113), the fp16 `-k fused`
 // path of mla.py (mla.py:177-179).
-at::Tensor mla_decode_split(const at::Tensor &query, const at::Tensor &cache, int64_t num_splits)
+at::Tensor mla_decode_split(const at::Tensor &query, const at::Tensor &cache, int64_t num_splits,
+                            double cache_scale)
 {
-    return decode_single(query, cache, num_splits, "mla_decode_split");
+    return decode_single(query, cache, num_splits, cache_scale, "mla_decode_split");
 }
 
 // Reference: mla_decode_fused (csrc/mla_api.cpp:34-54), the `-k fused --fp32`
 // path of mla.py (mla.py:174-176).
 at::Tensor mla_decode_fused(const at::Tensor &query, const at::Tensor &cache, int64_t num_splits)
 {
-    return decode_single(query, cache, num_splits, "mla_decode_fused");
+    TORCH_CHECK(cache.scalar_type() != at::kFloat8_e4m3fn, "mla_decode_fused: fp8 caches go through mla_decode_split");
+    return decode_single(query, cache, num_splits, 1.0, "mla_decode_fused");
 }
 
 // No reference counterpart: B independent sequences packed back to back.
 at::Tensor mla_decode_split_batched(const at::Tensor &query_in, const at::Tensor &cache_in,
-                                    const at::Tensor &cu_seqlens_in, int64_t num_splits)
+                                    const at::Tensor &cu_seqlens_in, int64_t num_splits, double cache_scale)
 {
     const char *fn = "mla_decode_split_batched";
-    TORCH_CHECK(query_in.scalar_type() == cache_in.scalar_type() &&
-                    (query_in.scalar_type() == at::kHalf || query_in.scalar_type() == at::kBFloat16),
-                fn, ": query and cache must both be float16 or both bfloat16");
+    const bool fp8 = is_fp8_cache(query_in, cache_in);
+    TORCH_CHECK(fp8 || (query_in.scalar_type() == cache_in.scalar_type() &&
+                        (query_in.scalar_type() == at::kHalf || query_in.scalar_type() == at::kBFloat16)),
+                fn, ": query and cache must both be float16 or both bfloat16 (or a float16 query with a "
+                "float8_e4m3fn cache)");
+    if (fp8)
+        check_cache_scale(cache_scale, fn);
     TORCH_CHECK(cu_seqlens_in.scalar_type() == at::kInt && cu_seqlens_in.dim() == 1, fn,
                 ": cu_seqlens must be a 1-D int32 tensor");
     TORCH_CHECK(query_in.dim() == 3 && query_in.size(2) == MLA_HEAD_DIM_K, fn,
@@ -145,12 +178,21 @@ at::Tensor mla_decode_split_batched(const at::Tensor &query_in, const at::Tensor
     const int total = static_cast<int>(cache.size(0));
     const int splits = static_cast<int>(num_splits);
     at::Tensor out = at::empty({batch, nh, MLA_HEAD_DIM_V}, query.options());
-    const size_t ws_bytes = mla_decode_split_batched_workspace_size(batch, nh, total, splits);
+    const size_t ws_bytes = fp8 ? mla_decode_split_fp8_workspace_size(batch, nh, total, splits)
+                                : mla_decode_split_batched_workspace_size(batch, nh, total, splits);
     TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
     at::Tensor ws = workspace(ws_bytes, query);
-    auto f = query.scalar_type() == at::kHalf ? mla_decode_split_batched_fp16 : mla_decode_split_batched_bf16;
-    const int st = f(query.data_ptr(), total > 0 ? cache.data_ptr() : nullptr, cu.data_ptr<int>(),
-                     out.data_ptr(), ws.data_ptr(), ws_bytes, batch, nh, total, splits, stream_of(query));
+    const void *c = total > 0 ? cache.data_ptr() : nullptr;
+    int st;
+    if (fp8) {
+        st = mla_decode_split_batched_fp8(query.data_ptr(), c, static_cast<float>(cache_scale), cu.data_ptr<int>(),
+                                          out.data_ptr(), ws.data_ptr(), ws_bytes, batch, nh, total, splits,
+                                          stream_of(query));
+    } else {
+        auto f = query.scalar_type() == at::kHalf ? mla_decode_split_batched_fp16 : mla_decode_split_batched_bf16;
+        st = f(query.data_ptr(), c, cu.data_ptr<int>(), out.data_ptr(), ws.data_ptr(), ws_bytes, batch, nh, total,
+               splits, stream_of(query));
+    }
     check_status(st, fn);
     return out;
 }
@@ -281,14 +323,17 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
 {
     m.doc() = "MI355X (gfx950) MLA decode: drop-in for the ada_mla extension's fused path";
     m.def("mla_decode_split", &mla_decode_split,
-          "fp16 / bf16 (or fp32) split-KV MLA decode (query [n_h,576], cache [N,576])",
-          pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("num_splits") = 0);
+          "fp16 / bf16 (or fp32) split-KV MLA decode (query [n_h,576], cache [N,576]); a float8_e4m3fn "
+          "cache (holding C / cache_scale) with a float16 query",
+          pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("num_splits") = 0,
+          pybind11::arg("cache_scale") = 1.0);
     m.def("mla_decode_fused", &mla_decode_fused, "fp32 MLA decode (query [n_h,576], cache [N,576])",
           pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("num_splits") = 0);
     m.def("mla_decode_split_batched", &mla_decode_split_batched,
-          "batched fp16 / bf16 MLA decode (query [B,n_h,576], packed cache [sum N,576], cu_seqlens [B+1] int32)",
+          "batched fp16 / bf16 MLA decode (query [B,n_h,576], packed cache [sum N,576], cu_seqlens [B+1] int32); "
+          "a float8_e4m3fn cache (holding C / cache_scale) with a float16 query",
           pybind11::arg("query"), pybind11::arg("cache"), pybind11::arg("cu_seqlens"),
-          pybind11::arg("num_splits") = 0);
+          pybind11::arg("num_splits") = 0, pybind11::arg("cache_scale") = 1.0);
     m.def("mla_decode_paged", &mla_decode_paged,
           "paged-KV fp16 / bf16 MLA decode (query [B,n_h,576], kv_cache [pages,page_size,576], "
           "block_table [B,max_pages] int32, cu_seqlens [B+1] int32)",

@@ -38,6 +38,9 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA
 MFMA_F32_PEAK_TFS = 157.3   # MI355X dense fp32 MFMA
 
+FP8_KINDS = ("fp8", "fp8_batched")
+BATCHED_KINDS = ("batched", "paged", "block", "fp8_batched")
+
 WORKLOADS = {
     "n4096": dict(kind="fp16", n_h=128, n=4096, desc="fp16 single sequence, n_h=128, N=4096 (BASELINE config 2)"),
     "n65536": dict(kind="fp16", n_h=128, n=65536, desc="fp16 split-KV, n_h=128, N=65536 (BASELINE config 3)"),
@@ -55,6 +58,9 @@ WORKLOADS = {
                                                  "n_h=128, N=4096 (fp8 variant of config 2)"),
     "fp8_n65536": dict(kind="fp8", n_h=128, n=65536, desc="fp8 (E4M3FN, per-tensor scale) KV cache, fp16 "
                                                           "query/output, n_h=128, N=65536 (fp8 variant of config 3)"),
+    "fp8_batched": dict(kind="fp8_batched", n_h=128, batch=32,
+                        desc="fp8 (E4M3FN, per-tensor scale) KV cache, fp16 query/output, batched B=32, "
+                             "N_b ~ U[512,16384] seed 42 (fp8 variant of config 5)"),
     "bf16": dict(kind="bf16", n_h=128, n=4096, desc="bf16 KV cache, n_h=128, N=4096 (bf16 variant of config 2)"),
 }
 
@@ -64,7 +70,7 @@ def algorithmic(kind, n_h, total_tokens, batch=1, d_model=0):
     step also the weights W_UK, W_UV [n_h,128,512], W_O [d_model, n_h*128], the query halves and
     the output read or written once, and their GEMM flops."""
     e = 4 if kind == "fp32" else 2
-    ec = 1 if kind == "fp8" else e  # cache bytes per value
+    ec = 1 if kind in FP8_KINDS else e  # cache bytes per value
     bytes_ = e * (batch * n_h * 576 + batch * n_h * 512) + ec * total_tokens * 576
     flops = 2 * n_h * total_tokens * (576 + 512)
     if kind == "block":
@@ -205,7 +211,9 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(42)
 
-    if kind in ("batched", "paged", "block"):
+    is_fp8 = kind in FP8_KINDS
+    c_dtype = torch.float8_e4m3fn if is_fp8 else None
+    if kind in BATCHED_KINDS:
         from ada_mla import synthetic
         seqlens = synthetic.batched_seqlens(wl["batch"], seed=42)
         batch = wl["batch"]
@@ -244,20 +252,16 @@ def main():
         batch, total = 1, wl["n"]
         q_shape, c_shape = (n_h, 576), (total, 576)
         dtype = {"fp32": torch.float32, "bf16": torch.bfloat16}.get(kind, torch.float16)
-        if kind == "fp8":
-            c_dtype = torch.float8_e4m3fn
     esz = 4 if dtype == torch.float32 else 2
     pair_bytes = (math.prod(q_shape) + math.prod(c_shape)) * esz
     pool = max(2, math.ceil(args.flush_mb * 2**20 / pair_bytes))
-    if kind == "fp8":
+    if is_fp8:
         pair_bytes = math.prod(q_shape) * esz + math.prod(c_shape)
         pool = max(2, math.ceil(args.flush_mb * 2**20 / pair_bytes))
     qs = [torch.randn(q_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
-    cs = [torch.randn(c_shape, generator=gen, device=dev, dtype=dtype if kind != "fp8" else torch.float32).to(
-        c_dtype) if kind == "fp8" else torch.randn(c_shape, generator=gen, device=dev, dtype=dtype)
-        for _ in range(pool)]
-    out = torch.empty((batch, n_h, 512) if kind in ("batched", "paged", "block") else (n_h, 512), device=dev,
-                      dtype=dtype)
+    cs = [torch.randn(c_shape, generator=gen, device=dev, dtype=torch.float32).to(c_dtype) if is_fp8 else
+          torch.randn(c_shape, generator=gen, device=dev, dtype=dtype) for _ in range(pool)]
+    out = torch.empty((batch, n_h, 512) if kind in BATCHED_KINDS else (n_h, 512), device=dev, dtype=dtype)
 
     splits = args.num_splits
     if kind in ("fp16", "bf16"):
@@ -271,8 +275,8 @@ def main():
     elif kind == "paged":
         ws_bytes = lib.mla_decode_paged_workspace_size(batch, n_h, total, splits)
         eff_splits = None
-    elif kind == "fp8":
-        ws_bytes = lib.mla_decode_split_fp8_workspace_size(1, n_h, total, splits)
+    elif is_fp8:
+        ws_bytes = lib.mla_decode_split_fp8_workspace_size(batch, n_h, total, splits)
         eff_splits = None
     elif kind == "block":
         ws_bytes = lib.mla_decode_split_batched_workspace_size(batch, n_h, total, splits)
@@ -299,6 +303,10 @@ def main():
         elif kind == "fp8":
             check(lib.mla_decode_split_fp8(q.data_ptr(), c.data_ptr(), 1.0, out.data_ptr(), ws.data_ptr(), ws_bytes,
                                            n_h, total, splits, sptr), "fp8")
+        elif kind == "fp8_batched":
+            check(lib.mla_decode_split_batched_fp8(q.data_ptr(), c.data_ptr(), 1.0, cu_d.data_ptr(), out.data_ptr(),
+                                                   ws.data_ptr(), ws_bytes, batch, n_h, total, splits, sptr),
+                  "fp8_batched")
         elif kind == "bf16":
             check(lib.mla_decode_split_bf16(q.data_ptr(), c.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_bytes,
                                             n_h, total, splits, sptr), "bf16")
@@ -421,7 +429,7 @@ def main():
         "roofline_time_us": max(bound_hbm, bound_mfma),
         "call_frac": max(bound_hbm, bound_mfma) / us_call,
     })
-    if kind in ("batched", "bf16", "paged", "block", "fp8"):
+    if kind in ("batched", "bf16", "paged", "block") + FP8_KINDS:
         roof["note"] = f"{kind} has no phase split: kernel_us is the whole call"
 
     res = {
@@ -436,12 +444,12 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"fp32": "fp32", "bf16": "bf16", "fp8": "fp16 (fp8 E4M3FN cache)"}.get(kind, "fp16"),
+        "dtype": "fp16 (fp8 E4M3FN cache)" if is_fp8 else {"fp32": "fp32", "bf16": "bf16"}.get(kind, "fp16"),
         "data": "synthetic (N(0,1), torch generator seed 42, resident in HBM)",
         "config": {
             "workload": wl["desc"],
             "num_heads": n_h,
-            "seq_len": total if kind not in ("batched", "paged", "block") else None,
+            "seq_len": total if kind not in BATCHED_KINDS else None,
             "total_tokens": total,
             "batch": batch,
             "num_splits": eff_splits,

@@ -146,6 +146,31 @@ def test_batched_extension_rejects_bad_inputs():
         m.mla_decode_split_batched(q.bfloat16(), c, torch.zeros(3, dtype=torch.int32))
 
 
+def test_fp8_extension_rejects_bad_inputs():
+    m = _ext()
+    q = torch.zeros(128, 576, dtype=torch.float16)
+    c8 = torch.zeros(64, 576, dtype=torch.float8_e4m3fn)
+    # fp8 caches pair with a float16 query only
+    with pytest.raises(RuntimeError, match="same dtype"):
+        m.mla_decode_split(q.bfloat16(), c8)
+    with pytest.raises(RuntimeError, match="cache_scale"):
+        m.mla_decode_split(q, c8, cache_scale=0.0)
+    with pytest.raises(RuntimeError, match="cache_scale"):
+        m.mla_decode_split(q, c8, cache_scale=float("inf"))
+    with pytest.raises(RuntimeError, match="go through mla_decode_split"):
+        m.mla_decode_fused(q, c8)
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        m.mla_decode_split(q, c8, cache_scale=0.5)
+    qb = torch.zeros(2, 128, 576, dtype=torch.float16)
+    cu = torch.zeros(3, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="cache_scale"):
+        m.mla_decode_split_batched(qb, c8, cu, cache_scale=-1.0)
+    with pytest.raises(RuntimeError, match="float8_e4m3fn"):
+        m.mla_decode_split_batched(qb.bfloat16(), c8, cu)
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        m.mla_decode_split_batched(qb, c8, cu, cache_scale=0.5)
+
+
 @pytest.mark.parametrize("fn", ["mla_decode_paged_fp16", "mla_decode_paged_bf16"])
 def test_paged_argument_errors(fn):
     lib = capi.load()

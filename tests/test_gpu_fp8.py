@@ -83,3 +83,24 @@ def test_fp8_batched_with_empty():
             assert not got[b].any()
         else:
             _check(got[b], ref[b], f"seq {b}")
+
+
+def test_fp8_extension_equals_c_abi():
+    # ada_mla.mla_decode_split / _batched with a float8_e4m3fn cache run the
+    # same kernels as the C ABI entries: results are bitwise equal
+    import ada_mla
+    q, c8, cd = _fp8_inputs(128, 2500, seed=21, scale=0.125)
+    qt, ct = torch.from_numpy(q).cuda(), c8.cuda()
+    a = ada_mla.mla_decode_split(qt, ct, cache_scale=0.125)
+    b = capi.decode_split_fp8(qt, ct, 0.125)
+    torch.cuda.synchronize()
+    assert a.dtype == torch.float16 and torch.equal(a, b)
+    _check(a.double().cpu().numpy(), O.closed_form(q, cd), "extension")
+    seqlens = np.array([40, 0, 2000])
+    qb, _, cu = synthetic.batched_inputs(16, seqlens, seed=22)
+    cb = torch.from_numpy(synthetic.normal((int(cu[-1]), 576), 23, np.float32)).to(torch.float8_e4m3fn).cuda()
+    qbt, cut = torch.from_numpy(qb).cuda(), torch.from_numpy(cu).cuda()
+    a = ada_mla.mla_decode_split_batched(qbt, cb, cut, num_splits=5, cache_scale=2.0)
+    b = capi.decode_split_batched_fp8(qbt, cb, 2.0, cut, num_splits=5)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
