@@ -327,10 +327,12 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             f8_to_f16(v);
     };
     // Prologue loads of a piece, issued by all 8 waves (wave w: C_N rows
-    // 4w..4w+3 and, for w < 4, the rope rows 8w..8w+7 of each block): Q* of
-    // the head tile into the top kQBlocks slots first, then blocks
-    // 0..kPre-1. Each wave waits for its own loads; the barrier after this
-    // (A) then publishes Q* and those blocks to every wave.
+    // 4w..4w+3 and, for w < 4, the rope rows 8w..8w+7 of each block, i.e.
+    // 5 load units per block for w < 4, else 4): Q* of the head tile into the top
+    // kQBlocks slots first, then blocks 0..kPre-1. Each wave waits for its
+    // own loads of Q* and block 0 only; the barrier after this (A) then
+    // publishes them to every wave, and blocks 1..kPre-1 land while block 0
+    // is computed (prologue_wait, and the feeders' first wait).
     auto prologue_loads = [&](int b, int seq_lo, int p_org, int p_hi) {
         const E *qb = q + ((size_t)b * num_heads + head0) * kDK;
 #pragma unroll
@@ -378,7 +380,24 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             if (wave < 4)
                 dma_rope(src, p_hi - 1 - t0, blk, wave);
         }
-        MLA_WAIT_VMCNT(0);
+        if (wave < 4)
+            MLA_WAIT_VMCNT(5 * (T::kPre - 1));
+        else
+            MLA_WAIT_VMCNT(4 * (T::kPre - 1));
+    };
+    // End of step t (t + 2 < kPre), for a wave whose only loads in flight
+    // are its prologue loads: its share of block t + 2 (the S waves' next
+    // block) has landed; the one after it may stay in flight.
+    static_assert(T::kPre >= 2 && T::kPre <= 3, "prologue blocks");
+    auto prologue_wait = [&](int t) {
+        if (t + 3 < T::kPre) {
+            if (wave < 4)
+                MLA_WAIT_VMCNT(5);
+            else
+                MLA_WAIT_VMCNT(4);
+        } else {
+            MLA_WAIT_VMCNT(0);
+        }
     };
 
     // Each role runs its own piece loop and step loop (t = -1 .. nblk-1: S
@@ -521,6 +540,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                             s_m[blk & 1][th][hrow] = mn;
                     }
                 }
+                if (t + 2 < T::kPre)
+                    prologue_wait(t);
                 lds_barrier();
             }
             // ---- epilogue: this half's running max and sum per head; the
@@ -575,10 +596,20 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     issue_unit(blk, k);
         };
         // End of step t: block t+2 (the S waves' next) must have landed;
-        // blocks t+3 and t+4 may stay in flight.
+        // blocks t+3 and t+4 may stay in flight. At t = -1 those are the
+        // prologue's blocks after block 1 (5 or 4 units each) and blocks
+        // kPre..3, issued after barrier B.
         auto feed_wait = [&](bool issued, int t) {
-            if (t < 0 || issued) MLA_WAIT_VMCNT(2 * T::kFeedUnits);
-            else MLA_WAIT_VMCNT(0);
+            if (t < 0) {
+                if (wave < 4)
+                    MLA_WAIT_VMCNT(5 * (T::kPre - 2) + (T::kRing - T::kPre) * T::kFeedUnits);
+                else
+                    MLA_WAIT_VMCNT(4 * (T::kPre - 2) + (T::kRing - T::kPre) * T::kFeedUnits);
+            } else if (issued) {
+                MLA_WAIT_VMCNT(2 * T::kFeedUnits);
+            } else {
+                MLA_WAIT_VMCNT(0);
+            }
         };
 
         if (wave >= T::kOWave0) {
@@ -720,6 +751,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     }
                     if constexpr (T::kOFeeds)
                         feed_wait(issue, t);
+                    else if (t + 2 < T::kPre)
+                        prologue_wait(t);
                     lds_barrier();
                 }
                 if (g == 0) {
