@@ -68,7 +68,10 @@ void set_chunks(Plan &p, int total_tokens, int batch, int w)
     p.chunk = ceil_div(ceil_div(total_tokens, w), p.block_tokens) * p.block_tokens;
     p.n_chunks = ceil_div(total_tokens, p.chunk);
     p.n_slots = p.n_chunks + batch - 1;
-    p.xcd_remap = (p.n_chunks % 8 == 0) ? 1 : 0;
+    // the launch grid is padded to a multiple of 8 chunks (the padding
+    // workgroups exit at once), so the head tiles of every chunk can share
+    // an XCD whatever n_chunks is
+    p.xcd_remap = 1;
 }
 
 // Modelled time of one 16-bit decode call (us) for a plan, fitted to MI355X
@@ -78,9 +81,10 @@ void set_chunks(Plan &p, int total_tokens, int batch, int w)
 // plus one at a step time that grows with the head tile (64: 1.5 us, 32:
 // 0.88 us, 16: 0.65 us with every CU busy), but no faster than streaming C
 // at ~6 TB/s; the partial round trip (written, then read by the combine)
-// at ~8 TB/s; and the combine's memory round trips. Head
-// tiles that share a chunk but not an XCD re-read C from HBM, which the
-// model charges as slower steps.
+// at ~8 TB/s; and the combine's memory round trips. Head tiles that
+// share a chunk but not an XCD (xcd_remap 0, which the planner no longer
+// produces) would re-read C from HBM; the model charges that as slower
+// steps.
 double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, int cu_count, bool paged)
 {
     const double step_us = p.head_tile == 64 ? 1.5 : p.head_tile == 32 ? 0.88 : 0.65;

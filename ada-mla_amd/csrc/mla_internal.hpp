@@ -25,10 +25,16 @@ struct Plan {
     int chunk;         // tokens per split (multiple of block_tokens)
     int n_chunks;      // splits over the packed tokens
     int n_slots;       // partial-result slots: n_chunks + batch - 1
-    int xcd_remap;     // 1: the head tiles of one chunk share an XCD
+    int xcd_remap;     // 1: the head tiles of one chunk share an XCD; the grid then
+                       // holds grid_chunks() chunks (n_chunks padded to a multiple of 8)
     int part_bytes;    // bytes per partial O element: 2 (16-bit paths), 4 (fp32 path, or 16-bit
                        // paths with fp32 partials)
 };
+
+// Chunks in the split kernels' launch grid: with xcd_remap, workgroup b
+// takes chunk (b / 8 / n_head_tiles) * 8 + b % 8, so the grid is padded to a
+// multiple of 8 chunks; the padding workgroups find no tokens and exit.
+inline int grid_chunks(const Plan &p) { return p.xcd_remap ? (p.n_chunks + 7) / 8 * 8 : p.n_chunks; }
 
 // Partial results of the split kernels: O in n_slots blocks of
 // num_heads x 512 elements, each stored as 16 x 16 tiles in MFMA accumulator

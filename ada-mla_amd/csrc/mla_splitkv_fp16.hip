@@ -194,6 +194,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     // chunk get ids that are equal mod 8, i.e. land on the same XCD (blocks
     // are dispatched round-robin over the 8 XCDs), so C is pulled from HBM
     // into that XCD's L2 once and re-read from L2 by the other head tiles.
+    // The grid then holds a multiple of 8 chunks; the padding workgroups
+    // (split >= n_chunks) return below.
     int split, ht;
     {
         const int bid = blockIdx.x;
@@ -206,10 +208,10 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             ht = bid - split * n_head_tiles;
         }
     }
+    if ((long long)split * chunk >= total_tokens)  // a padding workgroup of the grid
+        return;
     const int lo = split * chunk;
     const int hi = min(lo + chunk, total_tokens);
-    if (lo >= hi)
-        return;
     const int head0 = ht * HT;
 
     // First sequence containing token lo (largest b with cu[b] <= lo).
@@ -894,7 +896,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
 template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part = false, bool kF8 = false>
 hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStream_t s)
 {
-    const dim3 grid(p.n_chunks * p.n_head_tiles), block(F16Tile<HT>::kThreads);
+    const dim3 grid(grid_chunks(p) * p.n_head_tiles), block(F16Tile<HT>::kThreads);
     hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part, kF8>), grid, block, 0, s,
                        (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens, w.o, w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2, pb.paging, pb.out_scale);

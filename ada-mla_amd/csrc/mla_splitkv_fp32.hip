@@ -64,10 +64,10 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
             ht = bid - split * n_head_tiles;
         }
     }
+    if ((long long)split * chunk >= total_tokens)  // a padding workgroup of the grid
+        return;
     const int lo = split * chunk;
     const int hi = min(lo + chunk, total_tokens);
-    if (lo >= hi)
-        return;
     const int head0 = ht * kHT;
 
     int b = 0;
@@ -230,7 +230,7 @@ hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p, const Partials 
 {
     if (p.n_chunks == 0)
         return hipSuccess;
-    const dim3 grid(p.n_chunks * p.n_head_tiles), block(256);
+    const dim3 grid(grid_chunks(p) * p.n_head_tiles), block(256);
     hipLaunchKernelGGL(splitkv_fp32_kernel, grid, block, 0, s,
                        (const float *)pb.q, (const float *)pb.c, pb.cu_seqlens,
                        static_cast<float *>(w.o), w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
