@@ -216,12 +216,19 @@ void launch_part(const Problem &pb, const Plan &p, const Partials &w, int waves,
 }  // namespace
 
 // Waves that share one (tile, sequence) item: enough that each merges about
-// 4 slots of an average sequence, at most 16.
-int combine_waves_per_item(const Plan &p, int batch)
+// 4 slots of an average sequence, at most 16, and no more than keep the grid
+// to about kResidentWaves waves, so that it runs in one round. Measured on
+// MI355X (rocprofv3 kernel durations): batched B = 32 at n_h = 128 (8192
+// items, about 5 slots each) merges in 8.4 us with one wave per item against
+// 12.4 us with two; one sequence (256 items) is fastest with the 4-slot
+// rule (N = 4096: 8 waves per item).
+constexpr int kResidentWaves = 4096;
+
+int combine_waves_per_item(const Plan &p, int batch, int n_items)
 {
     const int slots = (p.n_slots + batch - 1) / batch;  // about the slots of one sequence
     int waves = 1;
-    while (waves < 16 && 4 * waves < slots)
+    while (waves < 16 && 4 * waves < slots && 2 * waves * n_items <= kResidentWaves)
         waves *= 2;
     return waves;
 }
@@ -230,7 +237,7 @@ hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
                           hipStream_t s)
 {
     const int n_items = pb.num_heads / 16 * (kDV / 16) * pb.batch;
-    const int waves = combine_waves_per_item(p, pb.batch);
+    const int waves = combine_waves_per_item(p, pb.batch, n_items);
     if (pb.fp32)
         launch_part<float, float>(pb, p, w, waves, n_items, s);
     else if (p.part_bytes == 4)
