@@ -20,6 +20,10 @@
 //    in flight while it merges the current 8, and the W wave results are
 //    merged through LDS. A workgroup holds max(8, W) waves, i.e. 8 / W items
 //    for W < 8.
+//  * with more items than the GPU keeps resident (large batches), one wave
+//    instead merges 4 consecutive tiles of a sequence (same heads), so one
+//    m / l load serves 4 tiles and the grid runs in one round
+//    (combine_tiles_kernel).
 #include <type_traits>
 
 #include "mla_device.hpp"
@@ -190,6 +194,137 @@ void combine_kernel(const PartT *__restrict__ o_part,
     }
 }
 
+// Many items (large batches): one wave merges kT consecutive tiles of one
+// sequence -- the same 16 heads, dims 16 * kT apart from the next wave's --
+// over all the sequence's slots, so the m and l loads serve kT tiles and each
+// wave keeps kT loads per slot in flight; 4 waves per workgroup. Slots go in
+// batches of kUT, the next batch's loads in flight while the current one
+// merges.
+constexpr int kT = 4;
+constexpr int kUT = 4;
+
+template <typename PartT, typename OutT>
+__global__ __launch_bounds__(256)
+void combine_tiles_kernel(const PartT *__restrict__ o_part,
+                          const float *__restrict__ m_part,
+                          const float *__restrict__ l_part,
+                          const int *__restrict__ cu_seqlens,
+                          void *__restrict__ out,
+                          int num_heads, int total_tokens, int chunk, int n_groups)
+{
+    constexpr bool kNorm = !std::is_same<OutT, float>::value;
+    using V = typename SlotBatch<PartT>::V;
+    struct Batch {
+        V v[kUT][kT];
+        float m[kUT];
+        float l[kUT];
+    };
+    const int lane = threadIdx.x & 63;
+    const int grp = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (grp >= n_groups)  // uniform per wave; no barriers follow
+        return;
+    constexpr int kGroupsPerHeads = kDV / 16 / kT;  // tile groups per 16 heads
+    const int groups_per_seq = num_heads / 16 * kGroupsPerHeads;
+    const int b = grp / groups_per_seq;
+    const int g = grp - b * groups_per_seq;
+    const int tile0 = (g / kGroupsPerHeads) * 32 + (g % kGroupsPerHeads) * kT;  // (head / 16) * 32 + dim / 16
+    const int head = (tile0 >> 5) * 16 + (lane & 15);
+
+    int lo = 0, hi = total_tokens;
+    if (cu_seqlens) {
+        lo = min(max(cu_seqlens[b], 0), total_tokens);
+        hi = min(max(cu_seqlens[b + 1], lo), total_tokens);
+    }
+    float m = -INFINITY, l = 0.f;
+    floatx4 acc[kT];
+#pragma unroll
+    for (int t = 0; t < kT; ++t)
+        acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (hi > lo) {
+        const int s0 = lo / chunk + b;
+        const int ns = (hi - 1) / chunk + b - s0 + 1;
+        const size_t slot_elems = (size_t)num_heads * kDV;
+        const PartT *op = o_part + (size_t)s0 * slot_elems + (size_t)tile0 * 256 + lane * 4;
+        const float *mp = m_part + (size_t)s0 * num_heads + head;
+        const float *lp = l_part + (size_t)s0 * num_heads + head;
+        auto load = [&](Batch &sb, int k0) {
+#pragma unroll
+            for (int j = 0; j < kUT; ++j) {
+                const int s = k0 + j;
+                if (s < ns) {
+#pragma unroll
+                    for (int t = 0; t < kT; ++t)
+                        sb.v[j][t] = *(const V *)(op + (size_t)s * slot_elems + t * 256);
+                    sb.m[j] = mp[(size_t)s * num_heads];
+                    sb.l[j] = lp[(size_t)s * num_heads];
+                } else {
+#pragma unroll
+                    for (int t = 0; t < kT; ++t)
+                        sb.v[j][t] = V{};
+                    sb.m[j] = -INFINITY;
+                    sb.l[j] = 0.f;
+                }
+            }
+        };
+        auto merge = [&](const Batch &sb) {
+            float mx = m;
+#pragma unroll
+            for (int j = 0; j < kUT; ++j)
+                mx = fmaxf(mx, sb.m[j]);
+            if (mx != -INFINITY) {  // uniform per wave: the first batch holds a slot
+                const float sc = fast_exp2(m - mx);
+                l *= sc;
+#pragma unroll
+                for (int t = 0; t < kT; ++t)
+                    acc[t] *= sc;
+#pragma unroll
+                for (int j = 0; j < kUT; ++j) {
+                    const float e = fast_exp2(sb.m[j] - mx);
+                    const float el = e * sb.l[j];
+#pragma unroll
+                    for (int t = 0; t < kT; ++t)
+                        acc[t] += (kNorm ? el : e) * to_f32(sb.v[j][t]);
+                    l += el;
+                }
+                m = mx;
+            }
+        };
+        Batch A, B;
+        int k0 = 0;
+        load(A, 0);
+        while (true) {
+            bool more = k0 + kUT < ns;
+            if (more)
+                load(B, k0 + kUT);
+            merge(A);
+            if (!more)
+                break;
+            k0 += kUT;
+            more = k0 + kUT < ns;
+            if (more)
+                load(A, k0 + kUT);
+            merge(B);
+            if (!more)
+                break;
+            k0 += kUT;
+        }
+    }
+    const float inv = (m != -INFINITY) ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+        const int dim0 = ((tile0 + t) & 31) * 16 + 4 * (lane >> 4);
+        const size_t o_off = ((size_t)b * num_heads + head) * kDV + dim0;
+        const floatx4 v = acc[t] * inv;
+        if constexpr (std::is_same<OutT, float>::value) {
+            *(floatx4 *)((float *)out + o_off) = v;
+        } else {
+            using VO = typename SlotBatch<OutT>::V;
+            const VO h = {(OutT)v[0], (OutT)v[1], (OutT)v[2], (OutT)v[3]};
+            *(VO *)((OutT *)out + o_off) = h;
+        }
+    }
+}
+
 template <typename PartT, typename OutT, int W>
 void launch_w(const Problem &pb, const Plan &p, const Partials &w, int n_items, hipStream_t s)
 {
@@ -204,6 +339,13 @@ template <typename PartT, typename OutT>
 void launch_part(const Problem &pb, const Plan &p, const Partials &w, int waves, int n_items,
                  hipStream_t s)
 {
+    if (waves == 0) {  // kT tiles per wave
+        const int n_groups = n_items / kT;
+        hipLaunchKernelGGL((combine_tiles_kernel<PartT, OutT>), dim3((n_groups + 3) / 4), dim3(256), 0, s,
+                           static_cast<const PartT *>(w.o), w.m, w.l, pb.cu_seqlens, pb.out, pb.num_heads,
+                           pb.total_tokens, p.chunk, n_groups);
+        return;
+    }
     switch (waves) {
     case 1: launch_w<PartT, OutT, 1>(pb, p, w, n_items, s); break;
     case 2: launch_w<PartT, OutT, 2>(pb, p, w, n_items, s); break;
@@ -226,6 +368,8 @@ constexpr int kResidentWaves = 4096;
 
 int combine_waves_per_item(const Plan &p, int batch, int n_items)
 {
+    if (n_items > kResidentWaves)
+        return 0;  // more items than resident waves: kT tiles per wave (combine_tiles_kernel)
     const int slots = (p.n_slots + batch - 1) / batch;  // about the slots of one sequence
     int waves = 1;
     while (waves < 16 && 4 * waves < slots && 2 * waves * n_items <= kResidentWaves)

@@ -81,6 +81,26 @@ def test_bf16_values_beyond_fp16_range():
            "scaled by 2^20")
 
 
+def test_bf16_batched_many_items_with_empty():
+    # 24 sequences x 128 heads: more combine items than resident waves, so
+    # each combine wave merges several tiles of a sequence
+    seqlens = np.random.default_rng(8).integers(2, 600, size=24)
+    seqlens[::5] = 0
+    seqlens[2] = 1
+    q32, c32, cu = synthetic.batched_inputs(128, seqlens, seed=10, dtype=np.float32)
+    q = torch.from_numpy(q32).to(torch.bfloat16)
+    c = torch.from_numpy(c32).to(torch.bfloat16)
+    out = capi.decode_split_batched_bf16(q.cuda(), c.cuda(), torch.from_numpy(cu).cuda(), num_splits=9)
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    ref = O.closed_form_batched(q.double().numpy(), c.double().numpy(), cu)
+    for b in range(len(seqlens)):
+        if seqlens[b] == 0:
+            assert not got[b].any()
+        else:
+            _check(got[b], ref[b], f"seq {b}")
+
+
 @pytest.mark.parametrize("splits", [0, 3])
 def test_bf16_batched_ragged_with_empty(splits):
     seqlens = np.array([5, 0, 17, 1, 300, 64, 0, 1000, 33])

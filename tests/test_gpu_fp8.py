@@ -85,6 +85,25 @@ def test_fp8_batched_with_empty():
             _check(got[b], ref[b], f"seq {b}")
 
 
+def test_fp8_batched_many_items_with_empty():
+    # 24 sequences x 128 heads: the combine merges several tiles per wave
+    seqlens = np.random.default_rng(6).integers(2, 600, size=24)
+    seqlens[1::6] = 0
+    q, _, cu = synthetic.batched_inputs(128, seqlens, seed=11)
+    c32 = synthetic.normal((int(cu[-1]), 576), 12, np.float32)
+    c8 = torch.from_numpy(c32 / np.float32(1.5)).to(torch.float8_e4m3fn)
+    cd = c8.float().double().numpy() * 1.5
+    out = capi.decode_split_batched_fp8(torch.from_numpy(q).cuda(), c8.cuda(), 1.5, torch.from_numpy(cu).cuda())
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    ref = O.closed_form_batched(q, cd, cu)
+    for b in range(len(seqlens)):
+        if seqlens[b] == 0:
+            assert not got[b].any()
+        else:
+            _check(got[b], ref[b], f"seq {b}")
+
+
 def test_fp8_extension_equals_c_abi():
     # ada_mla.mla_decode_split / _batched with a float8_e4m3fn cache run the
     # same kernels as the C ABI entries: results are bitwise equal

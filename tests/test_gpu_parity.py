@@ -217,6 +217,25 @@ def test_config5_batched():
         _check16(got[b], O.closed_form(q[b], c[lo:hi]), f"config 5 seq {b} N={hi - lo}")
 
 
+@pytest.mark.parametrize("n_h,batch,splits", [(128, 24, 0), (128, 24, 7), (128, 24, 200), (16, 160, 0), (48, 48, 13)])
+def test_batched_many_items_with_empty(n_h, batch, splits):
+    # more (16 x 16 tile, sequence) items than the combine keeps resident
+    # (4096): each combine wave merges several tiles of one sequence
+    rng = np.random.default_rng(31 + n_h + splits)
+    seqlens = rng.integers(2, 700, size=batch)
+    seqlens[::7] = 0
+    seqlens[3::11] = 1
+    seqlens[5] = 2500
+    q, c, cu = synthetic.batched_inputs(n_h, seqlens, seed=5)
+    got = _batched(q, c, cu, num_splits=splits)
+    ref = O.closed_form_batched(q, c, cu)
+    for b in range(batch):
+        if seqlens[b] == 0:
+            assert not got[b].any(), f"empty seq {b}"
+        else:
+            _check16(got[b], ref[b], f"seq {b} N={seqlens[b]}")
+
+
 def test_batched_equals_single_sequence_calls():
     seqlens = np.array([700, 129, 2048])
     q, c, cu = synthetic.batched_inputs(128, seqlens, seed=12)
