@@ -105,11 +105,12 @@ double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, in
 namespace {
 
 Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
-                  int num_splits, int cu_count, bool paged, bool f32_partials)
+                  int num_splits, int cu_count, CacheKind cache, bool f32_partials)
 {
+    const bool paged = cache != CacheKind::kPacked;  // pieces start page-aligned: one more block
     Plan p{};
     if (total_tokens <= 0) {
-        p.head_tile = fp32 ? 16 : (num_heads % 64 == 0 && !paged) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
+        p.head_tile = fp32 ? 16 : (num_heads % 64 == 0 && cache != CacheKind::kF8) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
         p.block_tokens = fp32 ? 16 : 32;
         p.n_head_tiles = num_heads / p.head_tile;
         p.chunk = p.block_tokens;
@@ -137,7 +138,7 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
     Plan best{};
     double best_us = 0.0;
     for (int ht : {64, 32, 16}) {
-        if (num_heads % ht != 0 || (paged && ht == 64))
+        if (num_heads % ht != 0 || (cache == CacheKind::kF8 && ht == 64))
             continue;
         Plan c{};
         c.head_tile = ht;
@@ -165,7 +166,7 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
 // time); decode loops repeat the same arguments, so each host thread keeps
 // its last few plans.
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
-               int num_splits, int cu_count, bool paged, bool f32_partials)
+               int num_splits, int cu_count, CacheKind kind, bool f32_partials)
 {
     struct Entry {
         int key[8];
@@ -174,7 +175,7 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
     constexpr int kEntries = 16;
     thread_local Entry cache[kEntries];
     thread_local int filled = 0, next = 0;
-    const int key[8] = {fp32, num_heads, total_tokens, batch, num_splits, cu_count, paged, f32_partials};
+    const int key[8] = {fp32, num_heads, total_tokens, batch, num_splits, cu_count, (int)kind, f32_partials};
     for (int e = 0; e < filled; ++e) {
         bool hit = true;
         for (int k = 0; k < 8; ++k)
@@ -182,7 +183,7 @@ Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
         if (hit)
             return cache[e].plan;
     }
-    const Plan p = compute_plan(fp32, num_heads, total_tokens, batch, num_splits, cu_count, paged, f32_partials);
+    const Plan p = compute_plan(fp32, num_heads, total_tokens, batch, num_splits, cu_count, kind, f32_partials);
     Entry &slot = cache[next];
     for (int k = 0; k < 8; ++k)
         slot.key[k] = key[k];
@@ -219,8 +220,8 @@ namespace {
 size_t split_workspace_bytes(int num_heads, int total_tokens, int batch, int num_splits)
 {
     const int cu = current_cu_count();
-    const Plan a = make_plan(false, num_heads, total_tokens, batch, num_splits, cu, false, false);
-    const Plan b = make_plan(false, num_heads, total_tokens, batch, num_splits, cu, false, true);
+    const Plan a = make_plan(false, num_heads, total_tokens, batch, num_splits, cu, CacheKind::kPacked, false);
+    const Plan b = make_plan(false, num_heads, total_tokens, batch, num_splits, cu, CacheKind::kPacked, true);
     return std::max(partials_bytes(a, num_heads), partials_bytes(b, num_heads));
 }
 
@@ -248,9 +249,9 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
         return MLA_STATUS_MISALIGNED;
     const bool fp32 = dt == Dtype::kF32;
     const bool f32_part = !fp32 && !paging && dt != Dtype::kF8Cache && (flags & MLA_FLAG_FP32_PARTIALS) != 0;
-    // the paged and fp8-cache kernels take tiles of 16 or 32 heads (planned like paged)
-    const Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, current_cu_count(),
-                             paging != nullptr || dt == Dtype::kF8Cache, f32_part);
+    const CacheKind kind = paging != nullptr ? CacheKind::kPaged
+                           : dt == Dtype::kF8Cache ? CacheKind::kF8 : CacheKind::kPacked;
+    const Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, current_cu_count(), kind, f32_part);
     if (workspace_bytes < partials_bytes(p, num_heads))
         return MLA_STATUS_WORKSPACE_TOO_SMALL;
 
@@ -310,7 +311,7 @@ int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits, u
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(), false,
+    return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
                           (flags & MLA_FLAG_FP32_PARTIALS) != 0)
         .n_chunks;
 }
@@ -407,7 +408,7 @@ size_t mla_decode_paged_workspace_size(int batch, int num_heads, int total_token
     if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
         return 0;
     const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, num_splits,
-                                       mla::current_cu_count(), true);
+                                       mla::current_cu_count(), mla::CacheKind::kPaged);
     return mla::partials_bytes(p, num_heads);
 }
 
@@ -457,7 +458,7 @@ size_t mla_decode_split_fp8_workspace_size(int batch, int num_heads, int total_t
     if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
         return 0;
     const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, num_splits,
-                                       mla::current_cu_count(), true);
+                                       mla::current_cu_count(), mla::CacheKind::kF8);
     return mla::partials_bytes(p, num_heads);
 }
 

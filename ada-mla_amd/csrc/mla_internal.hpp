@@ -75,10 +75,14 @@ struct Problem {
     float out_scale;        // multiplies the normalised partial O (c_scale for fp8, else 1)
 };
 
-// paged: head tiles of 16 or 32 only (the paged kernel needs dedicated
-// feeder waves) and one extra block per piece in the cost model.
+// Layout of the cache the plan is for. kPaged: one extra block per piece in
+// the cost model (pieces start page-aligned). kF8: the same, and head tiles
+// of 16 or 32 only (the fp8 cache is dequantised by dedicated feeder waves).
+enum class CacheKind { kPacked, kPaged, kF8 };
+
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
-               int num_splits, int cu_count, bool paged = false, bool f32_partials = false);
+               int num_splits, int cu_count, CacheKind cache = CacheKind::kPacked,
+               bool f32_partials = false);
 size_t partials_bytes(const Plan &p, int num_heads);
 Partials carve_partials(void *ws, const Plan &p, int num_heads);
 

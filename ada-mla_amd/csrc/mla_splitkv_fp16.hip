@@ -173,9 +173,6 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     using T = F16Tile<HT>;
     static_assert(!(kF8 && (kPaged || T::kOFeeds || !__is_same(E, _Float16))),
                   "fp8 cache: packed layout, fp16 ring, head tile of 16 or 32");
-    // paged caches are fed by dedicated feeder waves, which prefetch the
-    // page of the next block (the O waves of a 64-head tile do not)
-    static_assert(!(kPaged && T::kOFeeds), "paged cache needs a head tile of 16 or 32");
     using E8 = typename Vec<E>::v8;
     using E4 = typename Vec<E>::v4;
     __shared__ __attribute__((aligned(1024))) E s_ring[T::kRing * T::kSlot];
@@ -299,7 +296,6 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             return c + (size_t)t0 * kDK;
         }
     };
-    auto token_src = [&](int b, int seq_lo, int t0) { return src_at(page_of(b, seq_lo, t0), seq_lo, t0); };
     // fp8 cache: a staged unit is 8 bytes per lane, loaded into registers
     // and written to the ring as 8 fp16 values (16 bytes) -- the C_N part of
     // row `row` of the block at token t0 (lane -> logical chunk lane), or the
@@ -588,15 +584,6 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             else
                 dma_rope(base, lim, slot, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
         };
-        // After barrier B (the S waves hold Q* in registers) the feeders load
-        // blocks kPre..3 into the slots Q* used.
-        auto feed_rest = [&](auto &&issue_unit) {
-#pragma unroll
-            for (int blk = T::kPre; blk < T::kRing; ++blk)
-#pragma unroll
-                for (int k = 0; k < T::kFeedUnits; ++k)
-                    issue_unit(blk, k);
-        };
         // End of step t: block t+2 (the S waves' next) must have landed;
         // blocks t+3 and t+4 may stay in flight. At t = -1 those are the
         // prologue's blocks after block 1 (5 or 4 units each) and blocks
@@ -652,16 +639,37 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 const int nblk = (p_hi - p_org + T::kBT - 1) / T::kBT;
                 // unit k of this wave's share of block blk; a block past the
                 // last re-reads the last token only
-                auto issue_unit = [&](int blk, int k) {
-                    const int t0 = min(p_org + blk * T::kBT, p_hi - 1);
-                    load_unit(token_src(b, seq_lo, t0), p_hi - 1 - t0, blk % T::kRing, k);
+                auto t0_of = [&](int blk) { return min(p_org + blk * T::kBT, p_hi - 1); };
+                // unit k of this wave's share of block blk, whose first row is
+                // at src; a block past the last re-reads the last token only
+                auto issue_unit = [&](const E *src, int blk, int k) {
+                    load_unit(src, p_hi - 1 - t0_of(blk), blk % T::kRing, k);
                 };
                 lds_barrier();  // piece start
                 prologue_loads(b, seq_lo, p_org, p_hi);
+                // a paged cache's block-table reads: blocks kPre..3 before
+                // barrier B, then each step reads the page of the block the
+                // next step issues, so that the scalar load lands during a
+                // barrier (lds_barrier waits for it with the LDS counter)
+                int rest[T::kRing - T::kPre];
+                int next = 0;
+                if constexpr (T::kOFeeds) {
+#pragma unroll
+                    for (int blk = T::kPre; blk < T::kRing; ++blk)
+                        rest[blk - T::kPre] = page_of(b, seq_lo, t0_of(blk));
+                    next = page_of(b, seq_lo, t0_of(T::kRing));
+                }
                 lds_barrier();  // A
                 lds_barrier();  // B
-                if constexpr (T::kOFeeds)
-                    feed_rest(issue_unit);
+                if constexpr (T::kOFeeds) {
+#pragma unroll
+                    for (int blk = T::kPre; blk < T::kRing; ++blk) {
+                        const E *src = src_at(rest[blk - T::kPre], seq_lo, t0_of(blk));
+#pragma unroll
+                        for (int k = 0; k < T::kFeedUnits; ++k)
+                            issue_unit(src, blk, k);
+                    }
+                }
 
                 floatx4 o[T::kNHS][8];
                 float m_ref[T::kNHS];  // per head l16 of sub-tile hs: the accumulator's reference max
@@ -684,6 +692,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     // block t+4 goes into the slot of block t, which every
                     // wave has finished reading (its C_N^T fragments are in av)
                     const bool issue = T::kOFeeds && t >= 0 && t + T::kRing < nblk;
+                    // the page of block t+4 was read by the previous step
+                    const E *isrc = issue ? src_at(next, seq_lo, t0_of(t + T::kRing)) : c;
                     if (t >= 0) {
                         const int blk = t;
                         // ---- common reference max of the two token halves; P
@@ -730,6 +740,11 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                                 for (int dt = 0; dt < 8; ++dt)
                                     o[hs][dt] *= alpha[hs];
                         }
+                        // the page of the block the next step issues: read after
+                        // this step's P and max reads (a scalar load shares the
+                        // LDS counter), waited for at the step's barrier
+                        if (issue)
+                            next = page_of(b, seq_lo, t0_of(t + T::kRing + 1));
                         // ---- O^T[dims 128*ow .. +128][heads] += C_N^T P^T, with
                         // the next block's operand reads (and, when the O
                         // waves feed, this step's global->LDS loads) placed
@@ -742,13 +757,13 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                                 o[hs][dt] = mfma16x16x32(av[dt], pb[hs], o[hs][dt]);
                             av[dt] = load_av(cn, dt);
                             if (issue)
-                                issue_unit(blk + T::kRing, dt);
+                                issue_unit(isrc, blk + T::kRing, dt);
                             __builtin_amdgcn_sched_barrier(0);
                         }
                         if (issue) {
 #pragma unroll
                             for (int k = 8; k < T::kFeedUnits; ++k)
-                                issue_unit(blk + T::kRing, k);
+                                issue_unit(isrc, blk + T::kRing, k);
                         }
                     }
                     if constexpr (T::kOFeeds)
@@ -906,7 +921,9 @@ hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStr
 template <typename E>
 hipError_t launch_e(const Problem &pb, const Plan &p, const Partials &w, bool tr_load, hipStream_t s)
 {
-    if (pb.paging.block_table) {  // the plan keeps paged caches to tiles of 16 or 32 heads, fp16 partials
+    if (pb.paging.block_table) {  // fp16 / bf16 partials
+        if (p.head_tile == 64)
+            return tr_load ? launch_ht<64, true, E, true>(pb, p, w, s) : launch_ht<64, false, E, true>(pb, p, w, s);
         if (p.head_tile == 32)
             return tr_load ? launch_ht<32, true, E, true>(pb, p, w, s) : launch_ht<32, false, E, true>(pb, p, w, s);
         if (p.head_tile == 16)

@@ -75,6 +75,16 @@ def test_paged_bf16(page):
     _check_all(got, ref, n, 1e-2, f"bf16 page={page}")
 
 
+@pytest.mark.parametrize("page,dtype", [(32, torch.float16), (256, torch.float16), (64, torch.bfloat16)])
+def test_paged_long_sequences(page, dtype):
+    # long sequences at 128 heads: the planner takes 64-head tiles, whose O
+    # waves feed the ring and read the block table a step ahead
+    seqlens = [9000, 0, 15000, 33, 12000, 1, 8000, 16000]
+    print(f"paged long page={page} {dtype}", flush=True)
+    got, ref, n = _paged(128, seqlens, page, seed=page, dtype=dtype)
+    _check_all(got, ref, n, 5e-3 if dtype == torch.float16 else 1e-2, f"long page={page}")
+
+
 def test_paged_config5_shape():
     seqlens = synthetic.batched_seqlens(32, seed=42)
     print(f"paged config 5 total={int(seqlens.sum())}", flush=True)
