@@ -110,7 +110,7 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
     const bool paged = cache != CacheKind::kPacked;  // pieces start page-aligned: one more block
     Plan p{};
     if (total_tokens <= 0) {
-        p.head_tile = fp32 ? 16 : (num_heads % 64 == 0 && cache != CacheKind::kF8) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
+        p.head_tile = fp32 ? 16 : (num_heads % 64 == 0) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
         p.block_tokens = fp32 ? 16 : 32;
         p.n_head_tiles = num_heads / p.head_tile;
         p.chunk = p.block_tokens;
@@ -138,7 +138,7 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
     Plan best{};
     double best_us = 0.0;
     for (int ht : {64, 32, 16}) {
-        if (num_heads % ht != 0 || (cache == CacheKind::kF8 && ht == 64))
+        if (num_heads % ht != 0)
             continue;
         Plan c{};
         c.head_tile = ht;

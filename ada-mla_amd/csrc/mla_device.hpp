@@ -63,6 +63,17 @@ __device__ __forceinline__ typename Vec<E>::v4 lds_read_tr16(const E *p)
     return __builtin_bit_cast(typename Vec<E>::v4, r);
 }
 
+// ds_read_b64_tr_b8: within each group of 16 lanes, lane j points at the 8
+// bytes [row j / 2][8 * (j % 2) .. +7] of an 8 x 16 byte block; after the
+// read, lane i of the group holds column i of that block (byte r = row r).
+// (Lane layout measured on gfx950.)
+__device__ __forceinline__ uint2 lds_read_tr8(const unsigned char *p)
+{
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    const v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MLA_LDS v2i *)(const MLA_LDS unsigned char *)p);
+    return uint2{(unsigned)r[0], (unsigned)r[1]};
+}
+
 // 2^x on the hardware exp unit (v_exp_f32); 2^-inf = 0.
 __device__ __forceinline__ float fast_exp2(float x)
 {

@@ -49,6 +49,8 @@
 //    that issue them, so a barrier never drains the loads in flight.
 //  * The partial O is stored tile by tile in the MFMA accumulator order
 //    (frag_offset): every store instruction writes 512 B of contiguous memory.
+#include <type_traits>
+
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
 
@@ -121,6 +123,10 @@ __device__ __forceinline__ int rope_swizzle(int row)
     return (row >> 1) & 7;
 }
 
+// fp8 cache: byte offset of the rope parts within a ring slot (after 32
+// C_N rows of 512 bytes).
+constexpr int kF8Rope = 16384;
+
 // s_waitcnt vmcnt(n) leaving the other counters unconstrained.
 #define MLA_WAIT_VMCNT(n) \
     __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (7 << 4) | (0xF << 8))
@@ -155,9 +161,12 @@ __device__ __forceinline__ void global_to_lds16(const void *base, int off, const
 
 // kF32Part: the partial O is stored in fp32 (still normalised) instead of E.
 // kF8: the cache C is OCP fp8 (E4M3FN) [tokens][576] bytes and c points to
-// it (E is then fp16 for Q*, the ring and P); the feeder waves dequantise it
-// into the fp16 ring, exactly (every E4M3 value is an fp16 value), and the
-// per-tensor cache scale is folded into scale_log2 and out_scale.
+// it (E is then fp16 for Q* and P). The ring holds the fp8 bytes as loaded
+// (a block takes the first 18 KB of its slot; the load units are 512 bytes,
+// 32 lanes of a global->LDS load), so a CU fills half the bytes of a 16-bit
+// cache; the S and O waves convert their operands to fp16 after each LDS
+// read, exactly (every E4M3 value is an fp16 value). The per-tensor cache
+// scale is folded into scale_log2 and out_scale.
 template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part, bool kF8>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void splitkv_fp16_kernel(const E *__restrict__ q,
@@ -171,8 +180,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                          float out_scale)
 {
     using T = F16Tile<HT>;
-    static_assert(!(kF8 && (kPaged || T::kOFeeds || !__is_same(E, _Float16))),
-                  "fp8 cache: packed layout, fp16 ring, head tile of 16 or 32");
+    static_assert(!(kF8 && (kPaged || !__is_same(E, _Float16))), "fp8 cache: packed layout, fp16 query");
     using E8 = typename Vec<E>::v8;
     using E4 = typename Vec<E>::v4;
     __shared__ __attribute__((aligned(1024))) E s_ring[T::kRing * T::kSlot];
@@ -296,19 +304,33 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             return c + (size_t)t0 * kDK;
         }
     };
-    // fp8 cache: a staged unit is 8 bytes per lane, loaded into registers
-    // and written to the ring as 8 fp16 values (16 bytes) -- the C_N part of
-    // row `row` of the block at token t0 (lane -> logical chunk lane), or the
-    // rope part of rows 8*ru .. 8*ru+7 (lane -> row 8*ru + lane/8, logical
-    // chunk lane % 8). Rows past `lim` re-read row `lim`, as the loads above.
+    // fp8 ring slot (first 18 KB of a slot): the 512-byte C_N part of row r
+    // at byte 512 r, its 16-byte chunk c stored at c ^ (r mod 16); the
+    // 64-byte rope part at 16384 + 64 r, chunk c (0..3) at c ^ ((r / 4) mod 4).
+    // The first product's 8-byte row reads and the second's transpose reads
+    // (ds_read_b64_tr_b8) then touch 16 distinct 16-byte bank groups per 32
+    // lanes. A load unit is 32 lanes x 16 bytes: one C_N row, or the rope
+    // parts of 8 rows -- 36 units per block, as for a 16-bit cache.
     const unsigned char *c8 = reinterpret_cast<const unsigned char *>(c);
-    auto f8_load_row = [&](int t0, int lim, int row) -> uint2 {
-        return *(const uint2 *)(c8 + (size_t)(t0 + min(row, lim)) * kDK + 8 * lane);
+    unsigned char *ring8 = reinterpret_cast<unsigned char *>(s_ring);
+    auto dma_row8 = [&](const unsigned char *base, int lim, int slot, int row) {
+        if (lane < 32) {
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            global_to_lds16(base, min(row, lim) * kDK + 16 * (ln ^ row_swizzle(row)),
+                            ring8 + slot * (T::kSlot * 2) + row * kDV);
+        }
     };
-    auto f8_load_rope = [&](int t0, int lim, int ru) -> uint2 {
-        const int rrow = 8 * ru + (lane >> 3);
-        return *(const uint2 *)(c8 + (size_t)(t0 + min(rrow, lim)) * kDK + kDV + 8 * (lane & 7));
+    auto dma_rope8 = [&](const unsigned char *base, int lim, int slot, int ru) {
+        if (lane < 32) {
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int rrow = 8 * ru + (ln >> 2);
+            global_to_lds16(base, min(rrow, lim) * kDK + kDV + 16 * ((ln & 3) ^ ((rrow >> 2) & 3)),
+                            ring8 + slot * (T::kSlot * 2) + kF8Rope + 512 * ru);
+        }
     };
+    // 8 fp8 values -> 8 fp16 values (byte k -> element k)
     auto f8_to_f16 = [](uint2 v) -> half8 {
         const half2v a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v.x, 1.0f, false);
         const half2v b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v.x, 1.0f, true);
@@ -316,13 +338,24 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         const half2v e = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v.y, 1.0f, true);
         return half8{a[0], a[1], b[0], b[1], d[0], d[1], e[0], e[1]};
     };
-    auto f8_store_row = [&](uint2 v, int slot, int row) {
-        *(half8 *)(s_ring + slot * T::kSlot + row * kDV + 8 * (lane ^ row_swizzle(row))) = f8_to_f16(v);
+    // a block's load units for either cache type: src is its first row
+    auto block_src = [&](int page, int seq_lo, int t0) -> const void * {
+        if constexpr (kF8)
+            return c8 + (size_t)t0 * kDK;
+        else
+            return src_at(page, seq_lo, t0);
     };
-    auto f8_store_rope = [&](uint2 v, int slot, int ru) {
-        const int rrow = 8 * ru + (lane >> 3);
-        *(half8 *)(s_ring + slot * T::kSlot + T::kRope + rrow * (kDK - kDV) + 8 * ((lane & 7) ^ rope_swizzle(rrow))) =
-            f8_to_f16(v);
+    auto blk_row = [&](const void *src, int lim, int slot, int row) {
+        if constexpr (kF8)
+            dma_row8(static_cast<const unsigned char *>(src), lim, slot, row);
+        else
+            dma_row(static_cast<const E *>(src), lim, slot, row);
+    };
+    auto blk_rope = [&](const void *src, int lim, int slot, int ru) {
+        if constexpr (kF8)
+            dma_rope8(static_cast<const unsigned char *>(src), lim, slot, ru);
+        else
+            dma_rope(static_cast<const E *>(src), lim, slot, ru);
     };
     // Prologue loads of a piece, issued by all 8 waves (wave w: C_N rows
     // 4w..4w+3 and, for w < 4, the rope rows 8w..8w+7 of each block, i.e.
@@ -341,29 +374,6 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             if (wave < 4)
                 dma_rope(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, wave);
         }
-        if constexpr (kF8) {
-            // all loads first (in flight with Q*), then convert and store
-            uint2 v[T::kPre][5];
-#pragma unroll
-            for (int blk = 0; blk < T::kPre; ++blk) {
-                const int t0 = min(p_org + blk * T::kBT, p_hi - 1);
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    v[blk][r] = f8_load_row(t0, p_hi - 1 - t0, 4 * wave + r);
-                if (wave < 4)
-                    v[blk][4] = f8_load_rope(t0, p_hi - 1 - t0, wave);
-            }
-#pragma unroll
-            for (int blk = 0; blk < T::kPre; ++blk) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    f8_store_row(v[blk][r], blk, 4 * wave + r);
-                if (wave < 4)
-                    f8_store_rope(v[blk][4], blk, wave);
-            }
-            MLA_WAIT_VMCNT(0);
-            return;
-        }
         int pages[T::kPre];  // all page reads first: one wait for them all
 #pragma unroll
         for (int blk = 0; blk < T::kPre; ++blk)
@@ -371,12 +381,12 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
 #pragma unroll
         for (int blk = 0; blk < T::kPre; ++blk) {
             const int t0 = min(p_org + blk * T::kBT, p_hi - 1);
-            const E *src = src_at(pages[blk], seq_lo, t0);
+            const void *src = block_src(pages[blk], seq_lo, t0);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                dma_row(src, p_hi - 1 - t0, blk, 4 * wave + r);
+                blk_row(src, p_hi - 1 - t0, blk, 4 * wave + r);
             if (wave < 4)
-                dma_rope(src, p_hi - 1 - t0, blk, wave);
+                blk_rope(src, p_hi - 1 - t0, blk, wave);
         }
         if (wave < 4)
             MLA_WAIT_VMCNT(5 * (T::kPre - 1));
@@ -422,6 +432,15 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         auto a_at = [&](const E *slot, int r, int kk) -> E8 {
             return kk < 16 ? *(const E8 *)(slot + r * kDV + a_off[kk & 3] + 128 * (kk >> 2))
                            : *(const E8 *)(slot + r * (kDK - kDV) + a_off[kk - 12]);
+        };
+        // fp8 ring: the 8 bytes of K-step kk of row r (K = 32 kk + 8 g ..),
+        // converted only where the MFMA takes them, so that the read stays
+        // in flight
+        auto a8_raw = [&](const unsigned char *slot8, int r, int kk) -> uint2 {
+            const int ch = 2 * (kk & 15) + (g >> 1);  // 16-byte chunk within the C_N or rope part
+            return kk < 16 ? *(const uint2 *)(slot8 + r * kDV + 16 * (ch ^ row_swizzle(r)) + 8 * (g & 1))
+                           : *(const uint2 *)(slot8 + kF8Rope + r * (kDK - kDV) + 16 * (ch ^ ((r >> 2) & 3)) +
+                                              8 * (g & 1));
         };
 
         for_each_piece([&](int b, int seq_lo, int p_org, int p_lo, int p_hi) {
@@ -469,11 +488,17 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                             acc[ns][j] = floatx4{0.f, 0.f, 0.f, 0.f};
                     constexpr int kB = 3;                 // K-steps per batch
                     constexpr int kNB = kDK / 32 / kB;    // batches (6)
-                    E8 ab[3][kB];
+                    using AB = typename std::conditional<kF8, uint2, E8>::type;
+                    AB ab[3][kB];
+                    const unsigned char *cslot8 = ring8 + (blk % T::kRing) * (T::kSlot * 2);
                     auto load_batch = [&](int buf, int k0) {
 #pragma unroll
-                        for (int k = 0; k < kB; ++k)
-                            ab[buf][k] = a_at(cslot, 16 * th + l16, k0 + k);
+                        for (int k = 0; k < kB; ++k) {
+                            if constexpr (kF8)
+                                ab[buf][k] = a8_raw(cslot8, 16 * th + l16, k0 + k);
+                            else
+                                ab[buf][k] = a_at(cslot, 16 * th + l16, k0 + k);
+                        }
                     };
                     load_batch(0, 0);
                     load_batch(1, kB);
@@ -483,13 +508,18 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                             load_batch((bi + 2) % 3, (bi + 2) * kB);
                         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                        for (int k = 0; k < kB; ++k)
+                        for (int k = 0; k < kB; ++k) {
+                            E8 a;
+                            if constexpr (kF8)
+                                a = f8_to_f16(ab[bi % 3][k]);
+                            else
+                                a = ab[bi % 3][k];
 #pragma unroll
                             for (int ns = 0; ns < T::kNS; ++ns) {
                                 const int kk = bi * kB + k;
-                                acc[ns][kk % T::kChains] =
-                                    mfma16x16x32(ab[bi % 3][k], qf[ns][kk], acc[ns][kk % T::kChains]);
+                                acc[ns][kk % T::kChains] = mfma16x16x32(a, qf[ns][kk], acc[ns][kk % T::kChains]);
                             }
+                        }
                         __builtin_amdgcn_sched_barrier(0);
                     }
                     // ---- online softmax of this wave's 16 tokens, per head
@@ -530,10 +560,16 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         // 2(j - 4) + 1. This lane's tokens 4(g & 1) + i of
                         // group g >> 1 land in columns (i, i + 2) -> base,
                         // base + 1 and base + 4, base + 5.
-                        E *pw = s_p[blk & 1] + hrow * T::kPRow + 16 * th + 8 * (g >> 1) + 2 * (g & 1);
-                        using E2 = E __attribute__((ext_vector_type(2)));
-                        *(E2 *)pw = E2{ph[0], ph[2]};
-                        *(E2 *)(pw + 4) = E2{ph[1], ph[3]};
+                        if constexpr (kF8) {
+                            // the fp8 ring's transpose reads take the K (token)
+                            // order natural: tokens 4g .. 4g+3 of this half
+                            *(E4 *)(s_p[blk & 1] + hrow * T::kPRow + 16 * th + 4 * g) = ph;
+                        } else {
+                            E *pw = s_p[blk & 1] + hrow * T::kPRow + 16 * th + 8 * (g >> 1) + 2 * (g & 1);
+                            using E2 = E __attribute__((ext_vector_type(2)));
+                            *(E2 *)pw = E2{ph[0], ph[2]};
+                            *(E2 *)(pw + 4) = E2{ph[1], ph[3]};
+                        }
                         if (g == 0)
                             s_m[blk & 1][th][hrow] = mn;
                     }
@@ -578,11 +614,11 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         const int feeder = T::kOFeeds ? wave - T::kOWave0 : wave - T::kSWaves;
         // unit k (0..kFeedUnits-1) of this feeder's share of a block: C_N
         // row kFeedRows*feeder + k, or a rope unit of those rows
-        auto load_unit = [&](const E *base, int lim, int slot, int k) {
+        auto load_unit = [&](const void *base, int lim, int slot, int k) {
             if (k < T::kFeedRows)
-                dma_row(base, lim, slot, T::kFeedRows * feeder + k);
+                blk_row(base, lim, slot, T::kFeedRows * feeder + k);
             else
-                dma_rope(base, lim, slot, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
+                blk_rope(base, lim, slot, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
         };
         // End of step t: block t+2 (the S waves' next) must have landed;
         // blocks t+3 and t+4 may stay in flight. At t = -1 those are the
@@ -611,8 +647,27 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             if constexpr (T::kOFeeds)
                 __builtin_amdgcn_s_setprio(2);
             // C_N^T operand of dims 128*ow + 16*dt .. +15 from a ring slot
-            auto load_av = [&](const E *cs, int dt) -> E8 {
-                if constexpr (kTr) {
+            // fp8 ring: the raw bytes, converted where the MFMA takes them
+            using AV = typename std::conditional<kF8, uint2, E8>::type;
+            auto load_av = [&](const E *cs, int dt) -> AV {
+                if constexpr (kF8) {
+                    // lane (g, d): dim 128*ow + 16*dt + d of tokens 8g .. 8g+7
+                    // (K order natural); 16-byte chunk ch of the C_N rows
+                    const unsigned char *cs8 = reinterpret_cast<const unsigned char *>(cs);
+                    const int ch = 8 * ow + dt;
+                    if constexpr (kTr) {
+                        const int tok = 8 * g + (l16 >> 1);
+                        return lds_read_tr8(cs8 + tok * kDV + 16 * (ch ^ row_swizzle(tok)) + 8 * (l16 & 1));
+                    } else {
+                        unsigned w[2] = {0u, 0u};
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const int tok = 8 * g + j;
+                            w[j >> 2] |= (unsigned)cs8[tok * kDV + 16 * (ch ^ row_swizzle(tok)) + l16] << (8 * (j & 3));
+                        }
+                        return uint2{w[0], w[1]};
+                    }
+                } else if constexpr (kTr) {
                     // lane (g, j): K index 8g + j/4 (+4) is token row 8g + 2(j/4)
                     // (+1), dims 128*ow + 16*dt + 4*(j%4) .. +3
                     const int r0 = 8 * g + 2 * (l16 >> 2);
@@ -642,7 +697,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 auto t0_of = [&](int blk) { return min(p_org + blk * T::kBT, p_hi - 1); };
                 // unit k of this wave's share of block blk, whose first row is
                 // at src; a block past the last re-reads the last token only
-                auto issue_unit = [&](const E *src, int blk, int k) {
+                auto issue_unit = [&](const void *src, int blk, int k) {
                     load_unit(src, p_hi - 1 - t0_of(blk), blk % T::kRing, k);
                 };
                 lds_barrier();  // piece start
@@ -664,7 +719,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 if constexpr (T::kOFeeds) {
 #pragma unroll
                     for (int blk = T::kPre; blk < T::kRing; ++blk) {
-                        const E *src = src_at(rest[blk - T::kPre], seq_lo, t0_of(blk));
+                        const void *src = block_src(rest[blk - T::kPre], seq_lo, t0_of(blk));
 #pragma unroll
                         for (int k = 0; k < T::kFeedUnits; ++k)
                             issue_unit(src, blk, k);
@@ -683,7 +738,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 // C_N^T fragments of the block the next step accumulates; each
                 // step reloads them for its successor right after the MFMAs
                 // that consume them
-                E8 av[8];
+                AV av[8];
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt)
                     av[dt] = load_av(s_ring, dt);
@@ -693,7 +748,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     // wave has finished reading (its C_N^T fragments are in av)
                     const bool issue = T::kOFeeds && t >= 0 && t + T::kRing < nblk;
                     // the page of block t+4 was read by the previous step
-                    const E *isrc = issue ? src_at(next, seq_lo, t0_of(t + T::kRing)) : c;
+                    const void *isrc = issue ? block_src(next, seq_lo, t0_of(t + T::kRing)) : c;
                     if (t >= 0) {
                         const int blk = t;
                         // ---- common reference max of the two token halves; P
@@ -752,9 +807,14 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         const E *cn = s_ring + ((blk + 1) % T::kRing) * T::kSlot;
 #pragma unroll
                         for (int dt = 0; dt < 8; ++dt) {
+                            E8 a;
+                            if constexpr (kF8)
+                                a = f8_to_f16(av[dt]);
+                            else
+                                a = av[dt];
 #pragma unroll
                             for (int hs = 0; hs < T::kNHS; ++hs)
-                                o[hs][dt] = mfma16x16x32(av[dt], pb[hs], o[hs][dt]);
+                                o[hs][dt] = mfma16x16x32(a, pb[hs], o[hs][dt]);
                             av[dt] = load_av(cn, dt);
                             if (issue)
                                 issue_unit(isrc, blk + T::kRing, dt);
@@ -810,7 +870,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 // first token of block blk; a block past the last re-reads
                 // the last token only
                 auto t0_of = [&](int blk) { return min(p_org + blk * T::kBT, p_hi - 1); };
-                auto issue_block = [&](const E *src, int blk) {
+                auto issue_block = [&](const void *src, int blk) {
                     const int lim = p_hi - 1 - t0_of(blk);
 #pragma unroll
                     for (int k = 0; k < T::kFeedUnits; ++k)
@@ -818,67 +878,6 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 };
                 lds_barrier();  // piece start
                 prologue_loads(b, seq_lo, p_org, p_hi);
-                if constexpr (kF8) {
-                    // fp8 cache: this feeder's units of a block are staged in
-                    // registers two steps before they are converted and
-                    // written (block b in st[(b + 1) & 1]): step t writes
-                    // block t+4 (block 3 at step -1, after barrier B) and
-                    // stages block t+6. The steps in which both happen run in
-                    // a loop of their own, so that the loads in flight are the
-                    // same at each of its steps and the compiler's vmcnt waits
-                    // leave the next block's loads in flight; the last steps
-                    // of the piece (write only, or nothing) follow.
-                    uint2 st[2][T::kFeedUnits];
-                    auto f8_issue = [&](uint2(&buf)[T::kFeedUnits], int blk) {
-                        const int t0 = t0_of(blk), lim = p_hi - 1 - t0;
-#pragma unroll
-                        for (int k = 0; k < T::kFeedUnits; ++k)
-                            buf[k] = k < T::kFeedRows
-                                         ? f8_load_row(t0, lim, T::kFeedRows * feeder + k)
-                                         : f8_load_rope(t0, lim, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
-                    };
-                    auto f8_write = [&](const uint2(&buf)[T::kFeedUnits], int blk) {
-#pragma unroll
-                        for (int k = 0; k < T::kFeedUnits; ++k) {
-                            if (k < T::kFeedRows)
-                                f8_store_row(buf[k], blk % T::kRing, T::kFeedRows * feeder + k);
-                            else
-                                f8_store_rope(buf[k], blk % T::kRing, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
-                        }
-                    };
-                    static_assert(T::kPre == 3 && T::kRing == 4, "fp8 staging assumes one block after Q*");
-                    if (3 < nblk)
-                        f8_issue(st[0], 3);
-                    if (4 < nblk)
-                        f8_issue(st[1], 4);
-                    lds_barrier();  // A
-                    lds_barrier();  // B
-                    // step t: write block t+4 from st[(t + 1) & 1], then stage block t+6 there
-                    auto full_step = [&](int t, uint2(&buf)[T::kFeedUnits]) {
-                        f8_write(buf, t + T::kRing);
-                        f8_issue(buf, t + T::kRing + 2);
-                        lds_barrier();
-                    };
-                    auto tail_step = [&](int t, uint2(&buf)[T::kFeedUnits]) {
-                        if (t + T::kRing < nblk)
-                            f8_write(buf, t + T::kRing);
-                        if (t + T::kRing + 2 < nblk)
-                            f8_issue(buf, t + T::kRing + 2);
-                        lds_barrier();
-                    };
-                    int t = -1;
-                    for (; t + 1 + T::kRing + 2 < nblk; t += 2) {
-                        full_step(t, st[0]);
-                        full_step(t + 1, st[1]);
-                    }
-                    for (; t < nblk; t += 2) {
-                        tail_step(t, st[0]);
-                        if (t + 1 < nblk)
-                            tail_step(t + 1, st[1]);
-                    }
-                    lds_barrier();  // epilogue barrier of the S waves
-                    return;
-                }
                 // pages of blocks kPre..4, read before barrier B, and of each
                 // later block one step before it is issued, so that a paged
                 // cache's block-table reads arrive during a barrier
@@ -891,12 +890,12 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 lds_barrier();  // B
 #pragma unroll
                 for (int blk = T::kPre; blk < T::kRing; ++blk)
-                    issue_block(src_at(rest[blk - T::kPre], seq_lo, t0_of(blk)), blk);
+                    issue_block(block_src(rest[blk - T::kPre], seq_lo, t0_of(blk)), blk);
                 for (int t = -1; t < nblk; ++t) {
                     // block t+4 into the slot of block t
                     const bool issue = t >= 0 && t + T::kRing < nblk;
                     if (issue) {
-                        issue_block(src_at(next, seq_lo, t0_of(t + T::kRing)), t + T::kRing);
+                        issue_block(block_src(next, seq_lo, t0_of(t + T::kRing)), t + T::kRing);
                         next = page_of(b, seq_lo, t0_of(t + T::kRing + 1));
                     }
                     feed_wait(issue, t);
@@ -951,7 +950,10 @@ hipError_t launch_splitkv_fp16(const Problem &pb, const Plan &p, const Partials 
 {
     if (p.n_chunks == 0)
         return hipSuccess;
-    if (pb.fp8) {  // fp16 query, fp8 cache; the plan keeps tiles of 16 or 32 heads, fp16 partials
+    if (pb.fp8) {  // fp16 query, fp8 cache, fp16 partials
+        if (p.head_tile == 64)
+            return tr_load ? launch_ht<64, true, _Float16, false, false, true>(pb, p, w, s)
+                           : launch_ht<64, false, _Float16, false, false, true>(pb, p, w, s);
         if (p.head_tile == 32)
             return tr_load ? launch_ht<32, true, _Float16, false, false, true>(pb, p, w, s)
                            : launch_ht<32, false, _Float16, false, false, true>(pb, p, w, s);
