@@ -26,7 +26,7 @@ def _rand(shape, seed, scale, dtype):
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float16, 1e-2), (torch.bfloat16, 3e-2)])
-@pytest.mark.parametrize("b,n_h", [(1, 16), (5, 128), (32, 16)])
+@pytest.mark.parametrize("b,n_h", [(1, 16), (5, 128), (32, 16), (70, 32)])
 def test_absorb_query(dtype, tol, b, n_h):
     print(f"absorb {dtype} B={b} n_h={n_h}", flush=True)
     qn, qn_d = _rand((b, n_h, 128), 1, 1.0, dtype)
@@ -42,7 +42,7 @@ def test_absorb_query(dtype, tol, b, n_h):
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float16, 1e-2), (torch.bfloat16, 3e-2)])
-@pytest.mark.parametrize("b,n_h,d_model", [(1, 16, 256), (4, 128, 5120), (33, 16, 1000)])
+@pytest.mark.parametrize("b,n_h,d_model", [(1, 16, 256), (4, 128, 5120), (33, 16, 1000), (70, 32, 512)])
 def test_project_output(dtype, tol, b, n_h, d_model):
     print(f"project {dtype} B={b} n_h={n_h} d_model={d_model}", flush=True)
     o, o_d = _rand((b, n_h, 512), 4, 1.0, dtype)
