@@ -225,9 +225,11 @@ int mla_decode_split_batched_fp8(const void *query, const void *cache_fp8,
  *   -> out [batch][d_model] = concat_h(o_star[:, h] W_UV[h]^T) W_O^T, with
  *   the per-head values in a caller workspace of
  *   mla_project_output_workspace_size(batch, num_heads) bytes.
- * GEMMs run on rocBLAS (fp32 accumulation); the first call on a host thread
- * and device creates a rocBLAS handle, which allocates rocBLAS's own
- * workspace -- unlike the decode entry points, these may allocate once. */
+ * The W_UK and W_UV products are MFMA kernels of this library (fp32
+ * accumulation) and allocate nothing. The W_O GEMM runs on rocBLAS (fp32
+ * accumulation); the first mla_project_output_* call on a host thread and
+ * device creates a rocBLAS handle, which allocates rocBLAS's own workspace --
+ * unlike the decode entry points, that call may allocate once. */
 size_t mla_project_output_workspace_size(int batch, int num_heads);
 int mla_absorb_query_fp16(const void *q_nope, const void *q_rope,
                           const void *w_uk, void *q_star, int batch,
