@@ -76,8 +76,8 @@ struct Problem {
 };
 
 // Layout of the cache the plan is for. kPaged: one extra block per piece in
-// the cost model (pieces start page-aligned). kF8: the same, and head tiles
-// of 16 or 32 only (the fp8 cache is dequantised by dedicated feeder waves).
+// the cost model (pieces start page-aligned). kF8: charged the same extra
+// block, a stand-in for the operand conversions that lengthen its steps.
 enum class CacheKind { kPacked, kPaged, kF8 };
 
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,

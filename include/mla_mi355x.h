@@ -171,7 +171,7 @@ int mla_decode_split_batched_bf16(const void *query, const void *cache,
  * power of two >= 32. Page ids outside [0, num_pages) and block-table
  * columns beyond block_table_stride are clamped (the result is then
  * meaningless but every access stays inside the caller's buffers). The same
- * split planner as the packed batched entry, with head tiles of 16 or 32. */
+ * split planner as the packed batched entry (head tiles of 16, 32 or 64). */
 size_t mla_decode_paged_workspace_size(int batch, int num_heads,
                                        int total_tokens, int num_splits);
 int mla_decode_paged_fp16(const void *query, const void *kv_cache,
@@ -193,8 +193,9 @@ int mla_decode_paged_bf16(const void *query, const void *kv_cache,
  * work, README.md:408): query [.. x num_heads x 576] fp16, cache
  * [tokens x 576] OCP fp8 E4M3FN bytes holding C / cache_scale (a per-tensor
  * scale > 0), out fp16. The decode reads the cache at one byte per value
- * (half the HBM traffic of fp16) and dequantises it exactly into fp16 on the
- * way into LDS; products and softmax as on the fp16 path. Workspace from
+ * (half the HBM traffic of fp16), keeps the bytes as they are in LDS and
+ * converts each MFMA operand to fp16 after its LDS read (exact: every E4M3FN
+ * value is an fp16 value); products and softmax as on the fp16 path. Workspace from
  * mla_decode_split_fp8_workspace_size(batch, num_heads, total_tokens,
  * num_splits) (batch = 1 for the single-sequence entry). cu_seqlens as for
  * mla_decode_split_batched_fp16. */
