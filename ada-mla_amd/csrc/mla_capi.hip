@@ -40,6 +40,7 @@ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // split reads). Measured at 128 heads, N = 1024: 16.7 us per call with
 // 32-token splits (256 workgroups), 18.4 us with 64-token splits (128).
 constexpr int kMinSplitTokensF32 = 32;
+constexpr int kTwoPerCuTokensF32 = 256;
 
 constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
@@ -127,8 +128,16 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
         p.block_tokens = 16;
         p.n_head_tiles = num_heads / p.head_tile;
         int w = num_splits;
-        if (w <= 0)
-            w = std::min(cu_count / p.n_head_tiles, ceil_div(total_tokens, kMinSplitTokensF32));
+        if (w <= 0) {
+            // one workgroup per CU; two (the kernel's LDS and registers allow
+            // it) once each chunk still holds kTwoPerCuTokensF32 tokens.
+            // Measured at 128 heads: N = 16384 79.7 -> 66.6 us with two, while
+            // at N = 4096 (64-token chunks) two were slower (29.2 -> 30.8 us)
+            const int per_round = std::max(1, cu_count / p.n_head_tiles);
+            w = std::min(per_round, ceil_div(total_tokens, kMinSplitTokensF32));
+            if (total_tokens >= 2 * per_round * kTwoPerCuTokensF32)
+                w = 2 * per_round;
+        }
         set_chunks(p, total_tokens, batch, w);
         p.part_bytes = 4;
         return p;

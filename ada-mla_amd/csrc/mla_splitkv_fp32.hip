@@ -32,7 +32,7 @@ constexpr int kKQ = kDK / 4;             // K per wave (144)
 constexpr int kPRow = kBT + 4;
 static_assert(kBT * kRowChunks % 256 == 0, "stage split");
 
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void splitkv_fp32_kernel(const float *__restrict__ q,
                          const float *__restrict__ c,
                          const int *__restrict__ cu_seqlens,

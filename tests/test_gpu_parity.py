@@ -91,6 +91,15 @@ def test_fp32_shapes(n_h, n):
     _check32(_fp32(q, c), O.closed_form(q, c), f"n_h={n_h} N={n}")
 
 
+@pytest.mark.parametrize("n_h,n", [(128, 16384), (128, 20001), (32, 65536 + 7)])
+def test_fp32_two_workgroups_per_cu(n_h, n):
+    # long sequences: the fp32 plan puts two workgroups on each CU
+    print(f"fp32 n_h={n_h} N={n}", flush=True)
+    q, c = synthetic.decode_inputs(n_h, n, seed=300 + n)
+    q, c = q.astype(np.float32), c.astype(np.float32)
+    _check32(_fp32(q, c), O.closed_form(q, c), f"n_h={n_h} N={n}")
+
+
 def test_fp32_matches_c_restatement_of_reference_cpu_kernel():
     q, c = synthetic.decode_inputs(128, 1024, seed=7, dtype=np.float32)
     _check32(_fp32(q, c), O.naive_cpu(q, c), "vs naive_cpu")
