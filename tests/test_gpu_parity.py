@@ -100,6 +100,29 @@ def test_fp32_two_workgroups_per_cu(n_h, n):
     _check32(_fp32(q, c), O.closed_form(q, c), f"n_h={n_h} N={n}")
 
 
+@pytest.mark.parametrize("n_h", [1024, 4096])
+@pytest.mark.parametrize("n", [1, 200])
+def test_many_heads(n_h, n):
+    # up to the largest head count the entry points accept (4096): 64 head
+    # tiles of 64 heads, more combine items than resident waves
+    print(f"many heads n_h={n_h} N={n}", flush=True)
+    q, c = synthetic.decode_inputs(n_h, n, seed=400 + n)
+    ref = O.closed_form(q, c)
+    _check16(_fp16(q, c), ref, f"fp16 n_h={n_h} N={n}")
+    q32, c32 = q.astype(np.float32), c.astype(np.float32)
+    _check32(_fp32(q32, c32), O.closed_form(q32, c32), f"fp32 n_h={n_h} N={n}")
+
+
+def test_many_heads_batched():
+    lens = [130, 0, 1]
+    q, c, cu = synthetic.batched_inputs(4096, lens, seed=9)
+    out = capi.decode_split_batched_fp16(_t(q), _t(c), torch.from_numpy(cu).cuda())
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    _check16(got, O.closed_form_batched(q, c, cu), "batched n_h=4096")
+    assert (got[1] == 0).all()
+
+
 def test_fp32_matches_c_restatement_of_reference_cpu_kernel():
     q, c = synthetic.decode_inputs(128, 1024, seed=7, dtype=np.float32)
     _check32(_fp32(q, c), O.naive_cpu(q, c), "vs naive_cpu")
