@@ -15,7 +15,8 @@ around all K steps (value, us/call) and one pair around K back-to-back
 split-kernel launches (roofline.achieved for the dominant kernel).
 
 Prints ONE JSON line. --workload picks another configuration (n65536, nh16,
-batched, fp32) for measurement runs; the default is the headline one.
+batched, paged, block, bf16, the fp8 cache workloads, fp32 and fp32_n4096) for
+measurement runs; the default is the headline one.
 """
 from __future__ import annotations
 
@@ -48,6 +49,8 @@ WORKLOADS = {
     "batched": dict(kind="batched", n_h=128, batch=32,
                     desc="fp16 batched, B=32, N_b ~ U[512,16384] seed 42 (BASELINE config 5)"),
     "fp32": dict(kind="fp32", n_h=128, n=1024, desc="fp32 path, n_h=128, N=1024 (BASELINE config 1 shape on GPU)"),
+    "fp32_n4096": dict(kind="fp32", n_h=128, n=4096,
+                       desc="fp32 path, n_h=128, N=4096 (the length of the reference's --fp32 worklog figure)"),
     "paged": dict(kind="paged", n_h=128, batch=32, page=64,
                   desc="fp16 paged KV cache (64-token pages, shuffled), B=32, N_b ~ U[512,16384] seed 42 "
                        "(config 5 through a block table)"),
