@@ -163,7 +163,8 @@ __device__ __forceinline__ void global_to_lds16(const void *base, int off, const
 // kF8: the cache C is OCP fp8 (E4M3FN) [tokens][576] bytes and c points to
 // it (E is then fp16 for Q* and P). The ring holds the fp8 bytes as loaded
 // (a block takes the first 18 KB of its slot; the load units are 512 bytes,
-// 32 lanes of a global->LDS load), so a CU fills half the bytes of a 16-bit
+// 32 lanes of a global->LDS load, except for the dedicated feeders' 1 KB
+// units of two rows), so a CU fills half the bytes of a 16-bit
 // cache; the S and O waves convert their operands to fp16 after each LDS
 // read, exactly (every E4M3 value is an fp16 value). The per-tensor cache
 // scale is folded into scale_log2 and out_scale.
@@ -329,6 +330,24 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             global_to_lds16(base, min(rrow, lim) * kDK + kDV + 16 * ((ln & 3) ^ ((rrow >> 2) & 3)),
                             ring8 + slot * (T::kSlot * 2) + kF8Rope + 512 * ru);
         }
+    };
+    // fp8, one 64-lane load unit: C_N rows row0 and row0 + 1 (lanes 0-31 and
+    // 32-63; the two 512-byte rows are adjacent in the slot), or the rope
+    // parts of rows 16 rr .. 16 rr + 15 (1 KB). The dedicated feeders use
+    // these, so that a block takes 18 load instructions instead of 36.
+    auto dma_row8x2 = [&](const unsigned char *base, int lim, int slot, int row0) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int row = row0 + (ln >> 5);
+        global_to_lds16(base, min(row, lim) * kDK + 16 * ((ln & 31) ^ row_swizzle(row)),
+                        ring8 + slot * (T::kSlot * 2) + row0 * kDV);
+    };
+    auto dma_rope8x16 = [&](const unsigned char *base, int lim, int slot, int rr) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int rrow = 16 * rr + (ln >> 2);
+        global_to_lds16(base, min(rrow, lim) * kDK + kDV + 16 * ((ln & 3) ^ ((rrow >> 2) & 3)),
+                        ring8 + slot * (T::kSlot * 2) + kF8Rope + 1024 * rr);
     };
     // 8 fp8 values -> 8 fp16 values (byte k -> element k)
     auto f8_to_f16 = [](uint2 v) -> half8 {
@@ -612,13 +631,26 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         // lane % 8). The O waves feed at HT = 64; otherwise waves 2 and 3,
         // which have no other role, do.
         const int feeder = T::kOFeeds ? wave - T::kOWave0 : wave - T::kSWaves;
+        // fp8 with dedicated feeders: 64-lane units of two C_N rows (and 16
+        // rope rows), half the load instructions per block
+        constexpr bool kFeedPairs = kF8 && !T::kOFeeds;
+        constexpr int kFU = kFeedPairs ? T::kFeedRows / 2 + 1 : T::kFeedUnits;  // units per feeder and block
+        static_assert(!kFeedPairs || T::kFeedRows == 16, "paired fp8 units: 16 rows per feeder");
         // unit k (0..kFeedUnits-1) of this feeder's share of a block: C_N
         // row kFeedRows*feeder + k, or a rope unit of those rows
         auto load_unit = [&](const void *base, int lim, int slot, int k) {
-            if (k < T::kFeedRows)
+            if constexpr (kFeedPairs) {
+                // fp8, dedicated feeders: row pairs, then one 16-row rope unit
+                const unsigned char *b8 = static_cast<const unsigned char *>(base);
+                if (k < T::kFeedRows / 2)
+                    dma_row8x2(b8, lim, slot, T::kFeedRows * feeder + 2 * k);
+                else
+                    dma_rope8x16(b8, lim, slot, feeder);
+            } else if (k < T::kFeedRows) {
                 blk_row(base, lim, slot, T::kFeedRows * feeder + k);
-            else
+            } else {
                 blk_rope(base, lim, slot, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
+            }
         };
         // End of step t: block t+2 (the S waves' next) must have landed;
         // blocks t+3 and t+4 may stay in flight. At t = -1 those are the
@@ -627,11 +659,11 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         auto feed_wait = [&](bool issued, int t) {
             if (t < 0) {
                 if (wave < 4)
-                    MLA_WAIT_VMCNT(5 * (T::kPre - 2) + (T::kRing - T::kPre) * T::kFeedUnits);
+                    MLA_WAIT_VMCNT(5 * (T::kPre - 2) + (T::kRing - T::kPre) * kFU);
                 else
-                    MLA_WAIT_VMCNT(4 * (T::kPre - 2) + (T::kRing - T::kPre) * T::kFeedUnits);
+                    MLA_WAIT_VMCNT(4 * (T::kPre - 2) + (T::kRing - T::kPre) * kFU);
             } else if (issued) {
-                MLA_WAIT_VMCNT(2 * T::kFeedUnits);
+                MLA_WAIT_VMCNT(2 * kFU);
             } else {
                 MLA_WAIT_VMCNT(0);
             }
@@ -873,7 +905,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 auto issue_block = [&](const void *src, int blk) {
                     const int lim = p_hi - 1 - t0_of(blk);
 #pragma unroll
-                    for (int k = 0; k < T::kFeedUnits; ++k)
+                    for (int k = 0; k < kFU; ++k)
                         load_unit(src, lim, blk % T::kRing, k);
                 };
                 lds_barrier();  // piece start
