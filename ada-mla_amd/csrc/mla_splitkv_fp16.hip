@@ -163,8 +163,8 @@ __device__ __forceinline__ void global_to_lds16(const void *base, int off, const
 // kF8: the cache C is OCP fp8 (E4M3FN) [tokens][576] bytes and c points to
 // it (E is then fp16 for Q* and P). The ring holds the fp8 bytes as loaded
 // (a block takes the first 18 KB of its slot; the load units are 512 bytes,
-// 32 lanes of a global->LDS load, except for the dedicated feeders' 1 KB
-// units of two rows), so a CU fills half the bytes of a 16-bit
+// 32 lanes of a global->LDS load, except for the feeders' 1 KB units of
+// two rows), so a CU fills half the bytes of a 16-bit
 // cache; the S and O waves convert their operands to fp16 after each LDS
 // read, exactly (every E4M3 value is an fp16 value). The per-tensor cache
 // scale is folded into scale_log2 and out_scale.
@@ -631,11 +631,12 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         // lane % 8). The O waves feed at HT = 64; otherwise waves 2 and 3,
         // which have no other role, do.
         const int feeder = T::kOFeeds ? wave - T::kOWave0 : wave - T::kSWaves;
-        // fp8 with dedicated feeders: 64-lane units of two C_N rows (and 16
-        // rope rows), half the load instructions per block
-        constexpr bool kFeedPairs = kF8 && !T::kOFeeds;
+        // fp8: 64-lane units of two C_N rows (and, with the 16 rows of a
+        // dedicated feeder, of 16 rope rows), about half the load
+        // instructions per block
+        constexpr bool kFeedPairs = kF8;
         constexpr int kFU = kFeedPairs ? T::kFeedRows / 2 + 1 : T::kFeedUnits;  // units per feeder and block
-        static_assert(!kFeedPairs || T::kFeedRows == 16, "paired fp8 units: 16 rows per feeder");
+        static_assert(!kFeedPairs || T::kFeedRows == 16 || T::kFeedRows == 8, "paired fp8 units");
         // unit k (0..kFeedUnits-1) of this feeder's share of a block: C_N
         // row kFeedRows*feeder + k, or a rope unit of those rows
         auto load_unit = [&](const void *base, int lim, int slot, int k) {
@@ -645,7 +646,10 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 if (k < T::kFeedRows / 2)
                     dma_row8x2(b8, lim, slot, T::kFeedRows * feeder + 2 * k);
                 else
-                    dma_rope8x16(b8, lim, slot, feeder);
+                    if constexpr (T::kFeedRows == 16)
+                        dma_rope8x16(b8, lim, slot, feeder);
+                    else
+                        dma_rope8(b8, lim, slot, feeder);
             } else if (k < T::kFeedRows) {
                 blk_row(base, lim, slot, T::kFeedRows * feeder + k);
             } else {
@@ -753,7 +757,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     for (int blk = T::kPre; blk < T::kRing; ++blk) {
                         const void *src = block_src(rest[blk - T::kPre], seq_lo, t0_of(blk));
 #pragma unroll
-                        for (int k = 0; k < T::kFeedUnits; ++k)
+                        for (int k = 0; k < kFU; ++k)
                             issue_unit(src, blk, k);
                     }
                 }
@@ -848,13 +852,13 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                             for (int hs = 0; hs < T::kNHS; ++hs)
                                 o[hs][dt] = mfma16x16x32(a, pb[hs], o[hs][dt]);
                             av[dt] = load_av(cn, dt);
-                            if (issue)
+                            if (issue && dt < kFU)
                                 issue_unit(isrc, blk + T::kRing, dt);
                             __builtin_amdgcn_sched_barrier(0);
                         }
                         if (issue) {
 #pragma unroll
-                            for (int k = 8; k < T::kFeedUnits; ++k)
+                            for (int k = 8; k < kFU; ++k)
                                 issue_unit(isrc, blk + T::kRing, k);
                         }
                     }
