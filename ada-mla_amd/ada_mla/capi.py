@@ -21,6 +21,8 @@ STATUS_INVALID_VALUE = 1
 STATUS_MISALIGNED = 2
 STATUS_WORKSPACE_TOO_SMALL = 3
 STATUS_HIP_ERROR = 4
+STATUS_SCRATCH_EXCEEDED = 5
+NOALLOC_SCRATCH_BYTES = 32 << 20
 FLAG_SCALAR_TRANSPOSE = 1
 FLAG_FP32_PARTIALS = 4
 
@@ -33,6 +35,7 @@ _SIGNATURES = {
     "mla_decode_split_workspace_size": (_sz, [_i, _i, _i]),
     "mla_decode_split_fp16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "mla_decode_split_fp16_ex": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _u, _vp]),
+    "mla_decode_split_fp16_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "mla_decode_split_fp16_partials": (_i, [_vp, _vp, _vp, _sz, _i, _i, _i, _u, _vp]),
     "mla_decode_split_fp16_combine": (_i, [_vp, _sz, _vp, _i, _i, _i, _u, _vp]),
     "mla_decode_fused_workspace_size": (_sz, [_i, _i, _i]),

@@ -7,8 +7,15 @@
 #include <atomic>
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 
 #include "mla_internal.hpp"
+
+// Split partials of mla_decode_split_fp16_noalloc: a file-scope device array
+// of MLA_NOALLOC_SCRATCH_BYTES, one copy per GPU, held until the process ends.
+// Its name is a host-side stand-in: host code uses the device address that
+// hipGetSymbolAddress returns for the current device (noalloc_scratch below).
+static __device__ __align__(256) unsigned char scratch[MLA_NOALLOC_SCRATCH_BYTES];
 
 namespace mla {
 namespace {
@@ -297,6 +304,40 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
     return MLA_STATUS_SUCCESS;
 }
 
+// Device address of `scratch` on the current device, looked up with
+// hipGetSymbolAddress on the first call on each device and kept; nullptr
+// (the HIP error recorded) if the lookup fails.
+std::atomic<void *> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+void *noalloc_scratch()
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        fail_hip(e);
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        fail_hip(hipErrorInvalidDevice);
+        return nullptr;
+    }
+    void *p = g_scratch[dev].load(std::memory_order_acquire);
+    if (p)
+        return p;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fail_hip(e != hipSuccess ? e : hipErrorInvalidSymbol);
+            return nullptr;
+        }
+        g_scratch[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
 }  // namespace
 }  // namespace mla
 
@@ -312,6 +353,9 @@ const char *mla_status_string(int status)
     case MLA_STATUS_MISALIGNED: return "pointer not 16-byte aligned";
     case MLA_STATUS_WORKSPACE_TOO_SMALL: return "workspace too small";
     case MLA_STATUS_HIP_ERROR: return "HIP error";
+    case MLA_STATUS_SCRATCH_EXCEEDED:
+        return "the split partials need more than the allocation-free entry point's scratch "
+               "(MLA_NOALLOC_SCRATCH_BYTES); use mla_decode_split_fp16 with a workspace";
     default: return "unknown status";
     }
 }
@@ -351,6 +395,23 @@ int mla_decode_split_fp16(const void *query, const void *cache, void *out,
 {
     return mla_decode_split_fp16_ex(query, cache, out, workspace, workspace_bytes, num_heads,
                                     seq_length, num_splits, 0u, stream);
+}
+
+int mla_decode_split_fp16_noalloc(const void *query, const void *cache, void *out, int num_heads,
+                                  int seq_length, int num_splits, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return MLA_STATUS_INVALID_VALUE;
+    // the same plan as mla_decode_split_fp16; its partials must fit the scratch
+    const mla::Plan p = mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(),
+                                       mla::CacheKind::kPacked, false);
+    if (mla::partials_bytes(p, num_heads) > (size_t)MLA_NOALLOC_SCRATCH_BYTES)
+        return MLA_STATUS_SCRATCH_EXCEEDED;
+    void *ws = mla::noalloc_scratch();
+    if (!ws)
+        return MLA_STATUS_HIP_ERROR;
+    return mla::run_decode(mla::Dtype::kF16, query, cache, nullptr, out, ws, (size_t)MLA_NOALLOC_SCRATCH_BYTES, 1,
+                           num_heads, seq_length, num_splits, 0u, stream);
 }
 
 int mla_decode_split_fp16_partials(const void *query, const void *cache, void *workspace,

@@ -22,8 +22,10 @@
  *    split holds at least one LDS block).
  *  - Return value: MLA_STATUS_SUCCESS (0) or one of the codes below; nothing
  *    is enqueued when a code other than 0 or MLA_STATUS_HIP_ERROR is
- *    returned. Thread-safe: no global mutable state besides a per-device
- *    cache of the CU count and a thread-local last HIP error.
+ *    returned. Thread-safe. Shared state: a per-device cache of the CU
+ *    count and a per-device cache of the allocation-free entry point's
+ *    scratch address (each written once per device). Per host thread: the
+ *    last HIP error and the last few split plans.
  *  - num_heads must be a positive multiple of 16.
  */
 #ifndef MLA_MI355X_H
@@ -44,6 +46,11 @@ extern "C" {
 #define MLA_STATUS_MISALIGNED 2          /* a pointer is not 16-byte aligned */
 #define MLA_STATUS_WORKSPACE_TOO_SMALL 3 /* workspace_bytes below the size query */
 #define MLA_STATUS_HIP_ERROR 4           /* a HIP launch failed: mla_last_hip_error() */
+#define MLA_STATUS_SCRATCH_EXCEEDED 5    /* mla_decode_split_fp16_noalloc: partials exceed its scratch */
+
+/* Size of the device array that holds the split partials of
+ * mla_decode_split_fp16_noalloc (one per GPU the library runs on). */
+#define MLA_NOALLOC_SCRATCH_BYTES (32u << 20)
 
 /* Testing aid for mla_decode_split_fp16_ex: read the C_N^T operand of the
  * second product with scalar LDS loads instead of the LDS transpose read. */
@@ -92,6 +99,23 @@ int mla_decode_split_fp16_ex(const void *query, const void *cache, void *out,
                              void *workspace, size_t workspace_bytes,
                              int num_heads, int seq_length, int num_splits,
                              unsigned flags, void *stream);
+
+/* mla_decode_split_fp16 without a workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The split
+ * partials go to a file-scope device array of MLA_NOALLOC_SCRATCH_BYTES
+ * (32 MiB) that each GPU holds until the process ends; its device address is
+ * looked up (hipGetSymbolAddress) on the first call on each device. The call
+ * allocates nothing and launches the same kernels with the same split plan
+ * as mla_decode_split_fp16, so the results are identical. Every call on one
+ * GPU shares that GPU's array: calls that overlap in time on one GPU (other
+ * streams, other threads) race. Nothing in the array needs clearing: each
+ * call writes every partial it reads. Returns MLA_STATUS_SCRATCH_EXCEEDED
+ * when the plan's partials would not fit (not for any num_splits <= 0 plan
+ * on a GPU of up to 256 CUs: those stay below 17 MiB). */
+int mla_decode_split_fp16_noalloc(const void *query, const void *cache,
+                                  void *out, int num_heads, int seq_length,
+                                  int num_splits, void *stream);
 
 /* The two launches of mla_decode_split_fp16, one at a time: the split-KV
  * kernel, which leaves its partials in the workspace, then the LSE combine,

@@ -84,6 +84,21 @@ def test_split_fp16_argument_errors(args, code):
     assert capi.load().mla_decode_split_bf16(*args) == code
 
 
+def test_noalloc_argument_errors():
+    lib = capi.load()
+    f = lib.mla_decode_split_fp16_noalloc
+    assert f(FAKE, FAKE, FAKE, 24, 64, 0, None) == capi.STATUS_INVALID_VALUE
+    assert f(FAKE, FAKE, FAKE, 128, 0, 0, None) == capi.STATUS_INVALID_VALUE
+    # partials of 4096 heads x 256 splits (~1 GB) exceed the 32 MiB scratch: rejected
+    # before the scratch is looked up or anything launched
+    assert f(FAKE, FAKE, FAKE, 4096, 65536, 256, None) == capi.STATUS_SCRATCH_EXCEEDED
+    assert b"scratch" in lib.mla_status_string(capi.STATUS_SCRATCH_EXCEEDED)
+    # every plan the planner picks by itself for 128 heads fits (16 MiB + m, l at most)
+    for n in (1, 4096, 65536, 1 << 20):
+        splits = lib.mla_decode_split_num_splits(128, n, 0, 0)
+        assert splits * 128 * 512 * 2 < capi.NOALLOC_SCRATCH_BYTES
+
+
 def test_fused_fp32_rejects_head_dim():
     lib = capi.load()
     assert lib.mla_decode_fused_fp32(FAKE, FAKE, FAKE, FAKE, 1 << 30, 128, 512, 64, 0, None) == \
