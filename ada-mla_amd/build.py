@@ -64,8 +64,7 @@ def build_lib(jobs: int = 4) -> str:
                 print(out)
     lib = os.path.join(OUT_DIR, LIB_NAME)
     tmp = lib + ".tmp"
-    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp,
-          f"-L{os.path.join(ROCM, 'lib')}", "-lrocblas"])
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, lib)
     return lib
 

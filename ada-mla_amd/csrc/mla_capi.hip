@@ -61,13 +61,15 @@ float scale_log2()
     return (float)(1.4426950408889634 / std::sqrt(192.0));
 }
 
-int fail_hip(hipError_t e)
+int fail_hip(hipError_t e) { return record_hip_error(e); }
+
+}  // namespace
+
+int record_hip_error(hipError_t e)
 {
     t_last_hip_error = (int)e;
     return MLA_STATUS_HIP_ERROR;
 }
-
-}  // namespace
 
 namespace {
 

@@ -390,7 +390,9 @@ hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
     else
         pb.bf16 ? launch_part<__bf16, __bf16>(pb, p, w, waves, n_items, s)
                 : launch_part<_Float16, _Float16>(pb, p, w, waves, n_items, s);
-    return hipGetLastError();
+    // the launch's own error; hipPeekAtLastError leaves a sticky error from
+    // the caller's earlier work in place for the caller to see
+    return hipPeekAtLastError();
 }
 
 }  // namespace mla

@@ -80,6 +80,10 @@ struct Problem {
 // block, a stand-in for the operand conversions that lengthen its steps.
 enum class CacheKind { kPacked, kPaged, kF8 };
 
+// Records e as this host thread's last HIP error (mla_last_hip_error) and
+// returns MLA_STATUS_HIP_ERROR.
+int record_hip_error(hipError_t e);
+
 Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
                int num_splits, int cu_count, CacheKind cache = CacheKind::kPacked,
                bool f32_partials = false);

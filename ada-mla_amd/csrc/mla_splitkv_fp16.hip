@@ -881,7 +881,9 @@ hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStr
     hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part, kF8>), grid, block, 0, s,
                        (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens, w.o, w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2, pb.paging, pb.out_scale);
-    return hipGetLastError();
+    // the launch's own error; hipPeekAtLastError leaves a sticky error from
+    // the caller's earlier work in place for the caller to see
+    return hipPeekAtLastError();
 }
 
 template <typename E>

@@ -235,7 +235,9 @@ hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p, const Partials 
                        (const float *)pb.q, (const float *)pb.c, pb.cu_seqlens,
                        static_cast<float *>(w.o), w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2);
-    return hipGetLastError();
+    // the launch's own error; hipPeekAtLastError leaves a sticky error from
+    // the caller's earlier work in place for the caller to see
+    return hipPeekAtLastError();
 }
 
 }  // namespace mla

@@ -250,11 +250,10 @@ int mla_decode_split_batched_fp8(const void *query, const void *cache_fp8,
  *   -> out [batch][d_model] = concat_h(o_star[:, h] W_UV[h]^T) W_O^T, with
  *   the per-head values in a caller workspace of
  *   mla_project_output_workspace_size(batch, num_heads) bytes.
- * The W_UK and W_UV products are MFMA kernels of this library (fp32
- * accumulation) and allocate nothing. The W_O GEMM runs on rocBLAS (fp32
- * accumulation); the first mla_project_output_* call on a host thread and
- * device creates a rocBLAS handle, which allocates rocBLAS's own workspace --
- * unlike the decode entry points, that call may allocate once. */
+ * All three products are MFMA kernels of this library (fp32 accumulation)
+ * and allocate nothing: W_UK and W_UV one workgroup per (head, column
+ * slice), W_O streamed once from HBM through an LDS ring, 32 output columns
+ * per workgroup. */
 size_t mla_project_output_workspace_size(int batch, int num_heads);
 int mla_absorb_query_fp16(const void *q_nope, const void *q_rope,
                           const void *w_uk, void *q_star, int batch,

@@ -35,7 +35,7 @@ def _replay_check(fn, tensors, seed):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        fn()  # warm-up off the capture: plans, and the rocBLAS handle of the projection
+        fn()  # warm-up off the capture: plans
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
@@ -93,7 +93,7 @@ def test_graph_fp8_cache():
 
 
 def test_graph_block_step():
-    # absorption -> batched decode -> projections (W_O on rocBLAS) in one graph
+    # absorption -> batched decode -> projections in one graph
     b, n_h, d_model = 4, 32, 1024
     lens = [300, 17, 1000, 64]
     cu = torch.zeros(b + 1, dtype=torch.int32)
