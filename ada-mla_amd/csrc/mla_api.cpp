@@ -201,7 +201,10 @@ at::Tensor mla_decode_split_batched(const at::Tensor &query_in, const at::Tensor
 // addressed through block_table [batch, max_pages] (int32), with the
 // sequences' lengths as prefix sums cu_seqlens [batch + 1] (int32).
 // total_tokens (= cu_seqlens[batch]) is read from the device when not given,
-// which synchronises the stream.
+// which synchronises the stream. A given total_tokens is not checked against
+// cu_seqlens[batch]: sequences are clipped to [0, total_tokens), so a smaller
+// value silently truncates the trailing sequences; a larger one only changes
+// the split plan.
 at::Tensor mla_decode_paged(const at::Tensor &query_in, const at::Tensor &kv_in,
                             const at::Tensor &block_table_in, const at::Tensor &cu_seqlens_in,
                             int64_t total_tokens, int64_t num_splits)
@@ -336,7 +339,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
           pybind11::arg("num_splits") = 0, pybind11::arg("cache_scale") = 1.0);
     m.def("mla_decode_paged", &mla_decode_paged,
           "paged-KV fp16 / bf16 MLA decode (query [B,n_h,576], kv_cache [pages,page_size,576], "
-          "block_table [B,max_pages] int32, cu_seqlens [B+1] int32)",
+          "block_table [B,max_pages] int32, cu_seqlens [B+1] int32); total_tokens=-1 reads cu_seqlens[B] "
+          "(synchronising); a given total_tokens is not checked: one below cu_seqlens[B] silently "
+          "truncates the trailing sequences",
           pybind11::arg("query"), pybind11::arg("kv_cache"), pybind11::arg("block_table"),
           pybind11::arg("cu_seqlens"), pybind11::arg("total_tokens") = -1, pybind11::arg("num_splits") = 0);
     m.def("mla_absorb_query", &mla_absorb_query,

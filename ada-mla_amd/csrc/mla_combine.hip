@@ -384,9 +384,10 @@ hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
     const int waves = combine_waves_per_item(p, pb.batch, n_items);
     if (pb.fp32)
         launch_part<float, float>(pb, p, w, waves, n_items, s);
+    else if (p.part_bytes == 4 && !pb.bf16)  // fp32 partials: an option of the fp16 path only
+        launch_part<float, _Float16>(pb, p, w, waves, n_items, s);
     else if (p.part_bytes == 4)
-        pb.bf16 ? launch_part<float, __bf16>(pb, p, w, waves, n_items, s)
-                : launch_part<float, _Float16>(pb, p, w, waves, n_items, s);
+        return hipErrorInvalidValue;
     else
         pb.bf16 ? launch_part<__bf16, __bf16>(pb, p, w, waves, n_items, s)
                 : launch_part<_Float16, _Float16>(pb, p, w, waves, n_items, s);

@@ -49,6 +49,10 @@
 //    that issue them, so a barrier never drains the loads in flight.
 //  * The partial O is stored tile by tile in the MFMA accumulator order
 //    (frag_offset): every store instruction writes 512 B of contiguous memory.
+//    The partials (O, m, l) are written with nontemporal stores: they are read
+//    once, by the combine kernel, and kept out of the L2 they need not be
+//    written back from at the end of the kernel. Measured at N = 4096 (4.2 MB
+//    of partials): 12.78 -> 11.85 us per call.
 #include <type_traits>
 
 #include "mla_device.hpp"
@@ -548,8 +552,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     // and O share one scale
                     const float mr = s_mref[h];
                     const float ls = s_l[0][h] * fast_exp2(s_m[0][0][h] - mr) + s_l[1][h] * fast_exp2(s_m[0][1][h] - mr);
-                    m_part[(size_t)slot_out * num_heads + head0 + h] = mr;
-                    l_part[(size_t)slot_out * num_heads + head0 + h] = ls;
+                    __builtin_nontemporal_store(mr, m_part + (size_t)slot_out * num_heads + head0 + h);
+                    __builtin_nontemporal_store(ls, l_part + (size_t)slot_out * num_heads + head0 + h);
                 }
             }
         });
@@ -821,10 +825,10 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         const floatx4 v = o[hs][dt] * inv;
                         const size_t off = obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt);
                         if constexpr (kF32Part) {
-                            *(floatx4 *)((float *)o_part + off) = v;
+                            __builtin_nontemporal_store(v, (floatx4 *)((float *)o_part + off));
                         } else {
                             const E4 hv = {(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
-                            *(E4 *)((E *)o_part + off) = hv;
+                            __builtin_nontemporal_store(hv, (E4 *)((E *)o_part + off));
                         }
                     }
                 }
@@ -886,29 +890,15 @@ hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStr
     return hipPeekAtLastError();
 }
 
-template <typename E>
-hipError_t launch_e(const Problem &pb, const Plan &p, const Partials &w, bool tr_load, hipStream_t s)
+// one instantiation per head tile of a (cache type, partials) combination
+template <bool kTr, typename E, bool kPaged, bool kF32Part, bool kF8>
+hipError_t launch_tiles(const Problem &pb, const Plan &p, const Partials &w, hipStream_t s)
 {
-    if (pb.paging.block_table) {  // fp16 / bf16 partials
-        if (p.head_tile == 64)
-            return tr_load ? launch_ht<64, true, E, true>(pb, p, w, s) : launch_ht<64, false, E, true>(pb, p, w, s);
-        if (p.head_tile == 32)
-            return tr_load ? launch_ht<32, true, E, true>(pb, p, w, s) : launch_ht<32, false, E, true>(pb, p, w, s);
-        if (p.head_tile == 16)
-            return tr_load ? launch_ht<16, true, E, true>(pb, p, w, s) : launch_ht<16, false, E, true>(pb, p, w, s);
-        return hipErrorInvalidValue;
-    }
-    if (p.part_bytes == 4) {  // fp32 partials (packed layout only)
-        switch (p.head_tile) {
-        case 64: return tr_load ? launch_ht<64, true, E, false, true>(pb, p, w, s) : launch_ht<64, false, E, false, true>(pb, p, w, s);
-        case 32: return tr_load ? launch_ht<32, true, E, false, true>(pb, p, w, s) : launch_ht<32, false, E, false, true>(pb, p, w, s);
-        default: return tr_load ? launch_ht<16, true, E, false, true>(pb, p, w, s) : launch_ht<16, false, E, false, true>(pb, p, w, s);
-        }
-    }
     switch (p.head_tile) {
-    case 64: return tr_load ? launch_ht<64, true, E, false>(pb, p, w, s) : launch_ht<64, false, E, false>(pb, p, w, s);
-    case 32: return tr_load ? launch_ht<32, true, E, false>(pb, p, w, s) : launch_ht<32, false, E, false>(pb, p, w, s);
-    default: return tr_load ? launch_ht<16, true, E, false>(pb, p, w, s) : launch_ht<16, false, E, false>(pb, p, w, s);
+    case 64: return launch_ht<64, kTr, E, kPaged, kF32Part, kF8>(pb, p, w, s);
+    case 32: return launch_ht<32, kTr, E, kPaged, kF32Part, kF8>(pb, p, w, s);
+    case 16: return launch_ht<16, kTr, E, kPaged, kF32Part, kF8>(pb, p, w, s);
+    default: return hipErrorInvalidValue;
     }
 }
 
@@ -919,19 +909,25 @@ hipError_t launch_splitkv_fp16(const Problem &pb, const Plan &p, const Partials 
 {
     if (p.n_chunks == 0)
         return hipSuccess;
-    if (pb.fp8) {  // fp16 query, fp8 cache, fp16 partials
-        if (p.head_tile == 64)
-            return tr_load ? launch_ht<64, true, _Float16, false, false, true>(pb, p, w, s)
-                           : launch_ht<64, false, _Float16, false, false, true>(pb, p, w, s);
-        if (p.head_tile == 32)
-            return tr_load ? launch_ht<32, true, _Float16, false, false, true>(pb, p, w, s)
-                           : launch_ht<32, false, _Float16, false, false, true>(pb, p, w, s);
-        if (p.head_tile == 16)
-            return tr_load ? launch_ht<16, true, _Float16, false, false, true>(pb, p, w, s)
-                           : launch_ht<16, false, _Float16, false, false, true>(pb, p, w, s);
-        return hipErrorInvalidValue;
+    const bool f32_part = p.part_bytes == 4;
+    // The scalar transpose reads and fp32 partials are options of the packed
+    // fp16 entry points (their flags); the bf16, paged and fp8 caches are
+    // built with the LDS transpose read and 16-bit partials only.
+    if (!pb.bf16 && !pb.fp8 && !pb.paging.block_table) {
+        if (tr_load)
+            return f32_part ? launch_tiles<true, _Float16, false, true, false>(pb, p, w, s)
+                            : launch_tiles<true, _Float16, false, false, false>(pb, p, w, s);
+        return f32_part ? launch_tiles<false, _Float16, false, true, false>(pb, p, w, s)
+                        : launch_tiles<false, _Float16, false, false, false>(pb, p, w, s);
     }
-    return pb.bf16 ? launch_e<__bf16>(pb, p, w, tr_load, s) : launch_e<_Float16>(pb, p, w, tr_load, s);
+    if (!tr_load || f32_part)
+        return hipErrorInvalidValue;
+    if (pb.fp8)  // fp16 query, fp8 cache, fp16 partials
+        return launch_tiles<true, _Float16, false, false, true>(pb, p, w, s);
+    if (pb.paging.block_table)
+        return pb.bf16 ? launch_tiles<true, __bf16, true, false, false>(pb, p, w, s)
+                       : launch_tiles<true, _Float16, true, false, false>(pb, p, w, s);
+    return launch_tiles<true, __bf16, false, false, false>(pb, p, w, s);
 }
 
 }  // namespace mla

@@ -213,14 +213,16 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
 
         const float lsum = sum_over_lane_groups(l_run);
         if (tid < kHT) {
-            m_part[(size_t)slot * num_heads + head0 + tid] = m_run;
-            l_part[(size_t)slot * num_heads + head0 + tid] = lsum;
+            __builtin_nontemporal_store(m_run, m_part + (size_t)slot * num_heads + head0 + tid);
+            __builtin_nontemporal_store(lsum, l_part + (size_t)slot * num_heads + head0 + tid);
         }
-        // tile by tile in MFMA accumulator order: 1 KB of contiguous memory per store
+        // tile by tile in MFMA accumulator order: 1 KB of contiguous memory
+        // per store; nontemporal, as the partials are read once, by the
+        // combine (see mla_splitkv_fp16.hip)
         float *obase = o_part + (size_t)slot * num_heads * kDV + lane * 4;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
-            *(floatx4 *)(obase + frag_offset(head0, 128 * wave + 16 * dt)) = o[dt];
+            __builtin_nontemporal_store(o[dt], (floatx4 *)(obase + frag_offset(head0, 128 * wave + 16 * dt)));
     }
 }
 

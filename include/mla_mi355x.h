@@ -195,7 +195,13 @@ int mla_decode_split_batched_bf16(const void *query, const void *cache,
  * power of two >= 32. Page ids outside [0, num_pages) and block-table
  * columns beyond block_table_stride are clamped (the result is then
  * meaningless but every access stays inside the caller's buffers). The same
- * split planner as the packed batched entry (head tiles of 16, 32 or 64). */
+ * split planner as the packed batched entry (head tiles of 16, 32 or 64).
+ * total_tokens is not checked against cu_seqlens[batch] (that would need a
+ * device read): every sequence's range is clipped to [0, total_tokens), so a
+ * total_tokens below cu_seqlens[batch] silently truncates the trailing
+ * sequences (their rows cover only their tokens below total_tokens, zeros if
+ * none) and still returns MLA_STATUS_SUCCESS; a larger one only changes the
+ * split plan. */
 size_t mla_decode_paged_workspace_size(int batch, int num_heads,
                                        int total_tokens, int num_splits);
 int mla_decode_paged_fp16(const void *query, const void *kv_cache,
