@@ -45,7 +45,7 @@ _SIGNATURES = {
     "mla_decode_split_bf16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "mla_decode_split_batched_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "mla_decode_paged_workspace_size": (_sz, [_i, _i, _i, _i]),
-    "mla_project_output_workspace_size": (_sz, [_i, _i]),
+    "mla_project_output_workspace_size": (_sz, [_i, _i, _i]),
     "mla_decode_split_fp8_workspace_size": (_sz, [_i, _i, _i, _i]),
     "mla_decode_split_fp8": (_i, [_vp, _vp, ctypes.c_float, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "mla_decode_split_batched_fp8": (_i, [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
@@ -249,7 +249,7 @@ def project_output(o_star, w_uv, w_o, out=None):
     assert o_star.is_contiguous() and w_uv.is_contiguous() and w_o.is_contiguous()
     if out is None:
         out = torch.empty((b, d_model), dtype=o_star.dtype, device=o_star.device)
-    ws_bytes = lib.mla_project_output_workspace_size(b, n_h)
+    ws_bytes = lib.mla_project_output_workspace_size(b, n_h, d_model)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=o_star.device)
     fn = "mla_project_output_" + _suffix(o_star)
     _check(fn, getattr(lib, fn)(o_star.data_ptr(), w_uv.data_ptr(), w_o.data_ptr(), out.data_ptr(), ws.data_ptr(),

@@ -310,7 +310,7 @@ at::Tensor mla_project_output(const at::Tensor &o_in, const at::Tensor &w_uv_in,
     const at::Tensor o = o_in.contiguous(), wuv = w_uv_in.contiguous(), wo = w_o_in.contiguous();
     const int64_t d_model = wo.size(0);
     at::Tensor out = at::empty({b, d_model}, o.options());
-    const size_t ws_bytes = mla_project_output_workspace_size(static_cast<int>(b), static_cast<int>(nh));
+    const size_t ws_bytes = mla_project_output_workspace_size(static_cast<int>(b), static_cast<int>(nh), static_cast<int>(d_model));
     TORCH_CHECK(ws_bytes > 0, fn, ": unsupported sizes");
     at::Tensor ws = workspace(ws_bytes, o);
     auto f = dt == at::kHalf ? mla_project_output_fp16 : mla_project_output_bf16;

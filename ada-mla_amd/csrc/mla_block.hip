@@ -20,7 +20,9 @@
 // columns per workgroup. fp16 / bf16 inputs, fp32 accumulation. No
 // reference code exists for this part (the reference stops at the decode
 // kernel).
+#include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
@@ -177,119 +179,167 @@ __global__ __launch_bounds__(64) void value_proj_kernel(const E *__restrict__ o_
     }
 }
 
-// Output projection, one workgroup (4 waves) per 32 output columns n0 .. +31:
-//   out[b, n] = sum_k x[b, k] W_O[n, k]      (x = the value projection, [B x K])
-// as its transpose D[n][b] on 16x16x32 MFMAs, with W_O rows as the A operand
-// and x rows as the B operand, for rows b in groups of 32. Both stream
-// through a kStages-deep LDS ring in chunks of kChunk K: 32 rows of W_O and
-// 32 rows of x per stage, filled by direct global->LDS loads whose units are
-// 512 contiguous bytes of two rows each, so HBM sees long runs of W_O (which
-// is read once; x stays in L2 for every workgroup). Every load is one of
-// these, so the waits are explicit counts that leave the later stages in
-// flight. 16-byte chunk c of a 512-byte row sits at c ^ (row mod 16), which
-// spreads the operand reads (16 rows, one chunk each) over the LDS banks.
-// Wave w computes K-steps 2w and 2w + 1 of each chunk, and the four partial
-// tiles are summed through LDS. Columns past N and rows past B read clamped
-// addresses and are not stored.
-constexpr int kChunk = 256;   // K per ring stage (512 bytes of a row)
-constexpr int kStages = 4;    // ring stages (32 KB each: 16 KB of W_O, 16 KB of x)
-constexpr int kUnitsPerWave = 8;  // load units per wave and stage (4 of W_O, 4 of x)
+// Output projection:
+//   out[b, n] = sum_k x[b, k] W_O[n, k]      (x = the value projection, [B x K], K = n_h * 128)
+// as its transpose D[n][b] on 16x16x32 MFMAs, W_O rows the A operand and x
+// rows the B operand. W_O (168 MB at n_h = 128, d_model 5120) is the one
+// large operand and is streamed from HBM once.
+//  * Work: a unit is 64 output columns (64 rows of W_O) x 32 rows of x over
+//    all K, in kChunk-column chunks; the (unit, chunk) steps, units
+//    outermost, are cut into equal contiguous ranges, one per workgroup of a
+//    grid of at most one workgroup per CU (stream-K). Every CU thus streams
+//    the same share of W_O whatever d_model / 64 is (160 column blocks of 32
+//    on 256 CUs would leave 96 idle). A unit that one workgroup covers whole
+//    is stored directly; the pieces of a unit split between workgroups (at
+//    most a first and a last one per workgroup) are stored as fp32 partial
+//    tiles (nontemporal: read once) that reduce_units_kernel adds in a fixed
+//    order. (Adding them up in the kernel instead, by the last workgroup to
+//    finish a piece of the unit on agent-scope completion counters, measured
+//    slower: 40.3 us against 32.4 + 4.8 us for the two kernels, from the
+//    release / acquire cache maintenance.)
+//  * Within a workgroup the chunks run through one kStages-deep LDS ring
+//    with no break at unit boundaries: 64 rows of W_O and 32 rows of x per
+//    stage, filled by direct global->LDS loads of 512 contiguous bytes of two
+//    rows each. Every load is one of these, so the waits are explicit counts
+//    that leave the later stages in flight. 16-byte chunk c of a 512-byte row
+//    sits at c ^ (row mod 16), which spreads the operand reads (16 rows, one
+//    chunk each) over the LDS banks.
+//  * Wave w owns the 16 columns 16w .. +15 of the unit for both 16-row tiles
+//    of x over every K-step, so no sums cross waves. x (1 MB for B = 32 at
+//    n_h = 128) is re-read from L2 by every workgroup, half a byte per byte
+//    of W_O; measured, these x loads were the largest cost beside W_O itself.
+//  * K is a multiple of 128: a last chunk of 128 columns re-reads each row's
+//    last 16 valid bytes in place of the missing ones and skips its K-steps
+//    past K. Columns past N and rows past B read clamped addresses and are
+//    not stored.
+constexpr int kChunk = 256;        // K per ring stage (512 bytes of a row)
+constexpr int kStages = 3;         // ring stages (48 KB each: 32 KB of W_O, 16 KB of x)
+constexpr int kCols = 64;          // output columns (W_O rows) per unit
+constexpr int kUnitsPerWave = 12;  // load units per wave and stage (8 of W_O, 4 of x)
+constexpr int kMaxGrid = 512;      // workgroups of the output projection (partial slots: 2 each)
+constexpr int kPartTile = kCols * 32;  // floats of one partial tile [32 rows][64 columns]
+
+// the (unit, chunk) steps [g P, min(T, (g + 1) P)) of workgroup g
+struct OutProjGeom {
+    int n_blocks;  // column blocks of kCols
+    int chunks;    // K chunks per unit
+    int steps;     // T = units x chunks
+    int per_wg;    // P
+    int grid;
+};
 
 template <typename E>
 __global__ __launch_bounds__(256) void out_proj_kernel(const E *__restrict__ x, const E *__restrict__ w,
-                                                       E *__restrict__ out, int batch, int K, int N)
+                                                       E *__restrict__ out, float *__restrict__ part,
+                                                       int batch, int K, int N, OutProjGeom geo)
 {
     using E8 = typename Vec<E>::v8;
     using E4 = typename Vec<E>::v4;
-    constexpr int kRowHalves = kChunk;        // one row of a stage
-    constexpr int kPart = 32 * kRowHalves;    // halves: the W_O part (x part follows)
-    __shared__ __attribute__((aligned(1024))) E s_ring[kStages][2 * kPart];
-    __shared__ floatx4 s_red[4][2][2][64];  // [wave][column tile][row tile][lane]
+    constexpr int kRowHalves = kChunk;           // one row of a stage
+    constexpr int kXOff = kCols * kRowHalves;     // halves: x rows follow the W_O rows
+    constexpr int kStage = kXOff + 32 * kRowHalves;
+    __shared__ __attribute__((aligned(1024))) E s_ring[kStages][kStage];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: the load bases are scalars
     const int l16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 32;
-    const int nchunk = K / kChunk;
-    for (int b0 = 0; b0 < batch; b0 += 32) {
-        // load unit u (0..15) of a part: rows 2u, 2u + 1 (lanes 0-31, 32-63);
-        // lane: stored chunk position, fetching logical chunk
-        // (lane & 31) ^ (row mod 16)
-        auto unit = [&](const E *rows_base, int row_lim, int c, int st, int part, int u) {
-            int ln = lane;
-            asm volatile("" : "+v"(ln));
-            const int r = 2 * u + (ln >> 5);
-            const E *src = rows_base + (size_t)min(2 * u, row_lim) * K + (size_t)c * kChunk;
-            // rows 2u and 2u + 1 are K apart; a row past row_lim re-reads row_lim
-            const int dr = min(2 * u + 1, row_lim) - min(2 * u, row_lim);
-            global_to_lds16(src, (ln >> 5) * dr * K * 2 + 16 * ((ln & 31) ^ (r & 15)),
-                            &s_ring[st][part * kPart + 2 * u * kRowHalves]);
-        };
-        auto issue = [&](int c, int st) {
+    const int s_first = (int)blockIdx.x * geo.per_wg;
+    const int n_steps = min(geo.steps - s_first, geo.per_wg);
+
+    struct Step {
+        int unit, c, n0, b0;
+    };
+    auto step_at = [&](int j) -> Step {
+        Step st;
+        const int gs = s_first + j;
+        st.unit = __builtin_amdgcn_readfirstlane(gs / geo.chunks);
+        st.c = __builtin_amdgcn_readfirstlane(gs - st.unit * geo.chunks);
+        st.n0 = __builtin_amdgcn_readfirstlane((st.unit % geo.n_blocks) * kCols);
+        st.b0 = __builtin_amdgcn_readfirstlane((st.unit / geo.n_blocks) * 32);
+        return st;
+    };
+    // load unit u of a stage: rows 2u, 2u + 1 (lanes 0-31, 32-63) of the
+    // W_O part (u < 32) or of the x part; lane: stored chunk position,
+    // fetching logical chunk (lane & 31) ^ (row mod 16), at most the chunk's
+    // last valid one
+    auto unit = [&](const E *rows_base, int row_lim, int c, int st, int off, int u) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int r = 2 * u + (ln >> 5);
+        const int valid = min(kChunk, K - c * kChunk) / 8;  // 16-byte chunks of this K-chunk (16 or 32)
+        const E *src = rows_base + (size_t)min(2 * u, row_lim) * K + (size_t)c * kChunk;
+        // rows 2u and 2u + 1 are K apart; a row past row_lim re-reads row_lim
+        const int dr = min(2 * u + 1, row_lim) - min(2 * u, row_lim);
+        global_to_lds16(src, (ln >> 5) * dr * K * 2 + 16 * min((ln & 31) ^ (r & 15), valid - 1),
+                        &s_ring[st][off + 2 * u * kRowHalves]);
+    };
+    auto issue = [&](int j, int st) {
+        const Step sp = step_at(j);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                unit(w + (size_t)n0 * K, N - 1 - n0, c, st, 0, 4 * wave + i);
+        for (int i = 0; i < 8; ++i)
+            unit(w + (size_t)sp.n0 * K, N - 1 - sp.n0, sp.c, st, 0, 8 * wave + i);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                unit(x + (size_t)b0 * K, batch - 1 - b0, c, st, 1, 4 * wave + i);
-        };
-        // operand of K-step kk of rows 16 t + l16 of a part of stage st
-        auto op = [&](int st, int part, int t, int kk) -> E8 {
-            const int row = 16 * t + l16;
-            return *(const E8 *)(&s_ring[st][part * kPart + row * kRowHalves + 8 * ((4 * kk + g) ^ (row & 15))]);
-        };
-        floatx4 acc[2][2];
+        for (int i = 0; i < 4; ++i)
+            unit(x + (size_t)sp.b0 * K, batch - 1 - sp.b0, sp.c, st, kXOff, 4 * wave + i);
+    };
+    // operand of K-step kk of row `row` of the part at `off` of stage st
+    auto op = [&](int st, int off, int row, int kk) -> E8 {
+        return *(const E8 *)(&s_ring[st][off + row * kRowHalves + 8 * ((4 * kk + g) ^ (row & 15))]);
+    };
+    floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+    bool first_piece = true;  // the unit in progress is this workgroup's first
+    int piece_c0 = step_at(0).c;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+    for (int j = 0; j < kStages; ++j)
+        if (j < n_steps)
+            issue(j, j);
+    for (int j = 0; j < n_steps; ++j) {
+        const int st = j % kStages;
+        const Step sp = step_at(j);
+        // this wave's units of chunk j have landed (later stages may still be
+        // in flight; tile stores issued since are younger than them), then
+        // every wave's
+        const int after = min(kStages - 1, n_steps - 1 - j);
+        if (after >= 2)
+            MLA_WAIT_VMCNT(2 * kUnitsPerWave);
+        else if (after == 1)
+            MLA_WAIT_VMCNT(kUnitsPerWave);
+        else
+            MLA_WAIT_VMCNT(0);
+        lds_barrier();
+        auto ksteps = [&](auto n) {  // n K-steps of 32: 8, or 4 in a 128-column last chunk
 #pragma unroll
-            for (int bt = 0; bt < 2; ++bt)
-                acc[nt][bt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        __syncthreads();  // the ring and s_red are free (previous row group)
-#pragma unroll
-        for (int c = 0; c < kStages; ++c)
-            if (c < nchunk)
-                issue(c, c);
-        for (int c = 0; c < nchunk; ++c) {
-            const int st = c % kStages;
-            // this wave's units of chunk c have landed (later stages may still
-            // be in flight), then every wave's
-            const int after = min(kStages - 1, nchunk - 1 - c);
-            if (after >= 3)
-                MLA_WAIT_VMCNT(3 * kUnitsPerWave);
-            else if (after == 2)
-                MLA_WAIT_VMCNT(2 * kUnitsPerWave);
-            else if (after == 1)
-                MLA_WAIT_VMCNT(kUnitsPerWave);
-            else
-                MLA_WAIT_VMCNT(0);
-            lds_barrier();
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int kk = 2 * wave + k;
-                const E8 a0 = op(st, 0, 0, kk), a1 = op(st, 0, 1, kk);
-                const E8 x0 = op(st, 1, 0, kk), x1 = op(st, 1, 1, kk);
-                acc[0][0] = mfma16x16x32(a0, x0, acc[0][0]);
-                acc[0][1] = mfma16x16x32(a0, x1, acc[0][1]);
-                acc[1][0] = mfma16x16x32(a1, x0, acc[1][0]);
-                acc[1][1] = mfma16x16x32(a1, x1, acc[1][1]);
+            for (int kk = 0; kk < decltype(n)::value; ++kk) {
+                const E8 a = op(st, 0, 16 * wave + l16, kk);
+                const E8 x0 = op(st, kXOff, l16, kk), x1 = op(st, kXOff, 16 + l16, kk);
+                acc[0] = mfma16x16x32(a, x0, acc[0]);
+                acc[1] = mfma16x16x32(a, x1, acc[1]);
             }
-            lds_barrier();  // every wave has read stage st
-            if (c + kStages < nchunk)
-                issue(c + kStages, st);
-        }
-        // lane (g, b) of tile (nt, bt) holds D[n0 + 16 nt + 4 g .. +3][b0 + 16 bt + b]
+        };
+        if (K - sp.c * kChunk >= kChunk)
+            ksteps(std::integral_constant<int, kChunk / 32>{});
+        else
+            ksteps(std::integral_constant<int, kChunk / 64>{});
+        lds_barrier();  // every wave has read stage st
+        if (j + kStages < n_steps)
+            issue(j + kStages, st);
+        const bool unit_end = sp.c == geo.chunks - 1;
+        if (!unit_end && j != n_steps - 1)
+            continue;
+        // ---- end of this workgroup's piece of a unit: lane (g, b) of tile bt
+        // holds D[n0 + 16 wave + 4 g .. +3][b0 + 16 bt + b]
+        const bool whole = piece_c0 == 0 && unit_end;
+        const int slot = 2 * (int)blockIdx.x + (first_piece ? 0 : 1);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int bt = 0; bt < 2; ++bt)
-                s_red[wave][nt][bt][lane] = acc[nt][bt];
-        __syncthreads();
-        {
-            const int nt = wave >> 1, bt = wave & 1;
-            const floatx4 v = s_red[0][nt][bt][lane] + s_red[1][nt][bt][lane] + s_red[2][nt][bt][lane] +
-                              s_red[3][nt][bt][lane];
-            const int b = b0 + 16 * bt + l16;
-            const int n = n0 + 16 * nt + 4 * g;
-            if (b < batch) {
+        for (int bt = 0; bt < 2; ++bt) {
+            const floatx4 v = acc[bt];
+            acc[bt] = floatx4{0.f, 0.f, 0.f, 0.f};
+            const int bl = 16 * bt + l16;        // row within the unit
+            const int cl = 16 * wave + 4 * g;    // column within the unit
+            const int b = sp.b0 + bl, n = sp.n0 + cl;
+            if (!whole) {
+                // every row and column of the tile, so the sums stay in bounds
+                __builtin_nontemporal_store(v, (floatx4 *)(part + (size_t)slot * kPartTile + bl * kCols + cl));
+            } else if (b < batch) {
                 E *o = out + (size_t)b * N + n;
                 if (n + 3 < N && (N & 3) == 0) {
                     *(E4 *)o = E4{(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
@@ -301,8 +351,69 @@ __global__ __launch_bounds__(256) void out_proj_kernel(const E *__restrict__ x, 
                 }
             }
         }
+        first_piece = false;
+        piece_c0 = 0;
+    }
+
+}
+
+// out of the units split between workgroups: the sum of their pieces,
+// workgroup by workgroup (one thread per 4 columns of a row)
+template <typename E>
+__global__ __launch_bounds__(256) void reduce_units_kernel(const float *__restrict__ part, E *__restrict__ out,
+                                                           int batch, int N, OutProjGeom geo)
+{
+    using E4 = typename Vec<E>::v4;
+    const int quads = (N + 3) / 4;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= batch * quads)
+        return;
+    const int b = t / quads, n = 4 * (t - b * quads);
+    const int u = (b / 32) * geo.n_blocks + n / kCols;
+    const int g_lo = u * geo.chunks / geo.per_wg, g_hi = (u * geo.chunks + geo.chunks - 1) / geo.per_wg;
+    if (g_lo == g_hi)  // one workgroup covered the unit and stored it
+        return;
+    // the pieces in batches of 8 whose loads are all in flight before the
+    // sums (in workgroup order)
+    floatx4 v = {0.f, 0.f, 0.f, 0.f};
+    const float *tile0 = part + (b % 32) * kCols + n % kCols;
+    for (int g0 = g_lo; g0 <= g_hi; g0 += 8) {
+        floatx4 p[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int g = g0 + i;
+            const int slot = 2 * g + (u == g * geo.per_wg / geo.chunks ? 0 : 1);
+            p[i] = g <= g_hi ? __builtin_nontemporal_load((const floatx4 *)(tile0 + (size_t)slot * kPartTile))
+                             : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v += p[i];
+    }
+    E *o = out + (size_t)b * N + n;
+    if (n + 3 < N && (N & 3) == 0) {
+        *(E4 *)o = E4{(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (n + i < N)
+                o[i] = (E)v[i];
     }
 }
+
+OutProjGeom out_proj_geom(int batch, int K, int N, int cu_count)
+{
+    OutProjGeom geo;
+    geo.n_blocks = (N + kCols - 1) / kCols;
+    geo.chunks = (K + kChunk - 1) / kChunk;
+    geo.steps = geo.n_blocks * ((batch + 31) / 32) * geo.chunks;
+    const int grid = std::max(1, std::min({cu_count, kMaxGrid, geo.steps}));
+    geo.per_wg = (geo.steps + grid - 1) / grid;
+    geo.grid = (geo.steps + geo.per_wg - 1) / geo.per_wg;
+    return geo;
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 int absorb(bool bf16, const void *q_nope, const void *q_rope, const void *w_uk, void *q_star,
            int batch, int num_heads, void *stream)
@@ -333,27 +444,39 @@ int project(bool bf16, const void *o_star, const void *w_uv, const void *w_o, vo
         return MLA_STATUS_INVALID_VALUE;
     if (!aligned16(o_star) || !aligned16(w_uv) || !aligned16(w_o) || !aligned16(out) || !aligned16(workspace))
         return MLA_STATUS_MISALIGNED;
-    if (workspace_bytes < mla_project_output_workspace_size(batch, num_heads))
+    if (workspace_bytes < mla_project_output_workspace_size(batch, num_heads, d_model))
         return MLA_STATUS_WORKSPACE_TOO_SMALL;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int hv = num_heads * kNope;
-    // o [B x n_h*128] (the workspace): o[b, h*128 + j] = O*[b, h, :] . W_UV[h][j][:]
-    if (bf16)
+    // workspace: o [B x n_h*128] (16-bit), then the W_O kernel's partial tiles
+    const OutProjGeom geo = out_proj_geom(batch, hv, d_model, current_cu_count());
+    const bool split = geo.per_wg % geo.chunks != 0 && geo.grid > 1;  // some unit is shared
+    char *ws = static_cast<char *>(workspace);
+    float *part = reinterpret_cast<float *>(ws + align256((size_t)batch * hv * 2));
+    const int quads = batch * ((d_model + 3) / 4);
+    // o[b, h*128 + j] = O*[b, h, :] . W_UV[h][j][:], then
+    // out [B x d_model] = o W_O^T
+    if (bf16) {
         hipLaunchKernelGGL(value_proj_kernel<__bf16>, dim3(num_heads * 4), dim3(64), 0, s,
                            static_cast<const __bf16 *>(o_star), static_cast<const __bf16 *>(w_uv),
-                           static_cast<__bf16 *>(workspace), batch, num_heads);
-    else
+                           reinterpret_cast<__bf16 *>(ws), batch, num_heads);
+        hipLaunchKernelGGL(out_proj_kernel<__bf16>, dim3(geo.grid), dim3(256), 0, s,
+                           reinterpret_cast<const __bf16 *>(ws), static_cast<const __bf16 *>(w_o),
+                           static_cast<__bf16 *>(out), part, batch, hv, d_model, geo);
+        if (split)
+            hipLaunchKernelGGL(reduce_units_kernel<__bf16>, dim3((quads + 255) / 256), dim3(256), 0, s, part,
+                               static_cast<__bf16 *>(out), batch, d_model, geo);
+    } else {
         hipLaunchKernelGGL(value_proj_kernel<_Float16>, dim3(num_heads * 4), dim3(64), 0, s,
                            static_cast<const _Float16 *>(o_star), static_cast<const _Float16 *>(w_uv),
-                           static_cast<_Float16 *>(workspace), batch, num_heads);
-    // out [B x d_model] = o [B x n_h*128] W_O^T
-    const dim3 grid((d_model + 31) / 32);
-    if (bf16)
-        hipLaunchKernelGGL(out_proj_kernel<__bf16>, grid, dim3(256), 0, s, static_cast<const __bf16 *>(workspace),
-                           static_cast<const __bf16 *>(w_o), static_cast<__bf16 *>(out), batch, hv, d_model);
-    else
-        hipLaunchKernelGGL(out_proj_kernel<_Float16>, grid, dim3(256), 0, s, static_cast<const _Float16 *>(workspace),
-                           static_cast<const _Float16 *>(w_o), static_cast<_Float16 *>(out), batch, hv, d_model);
+                           reinterpret_cast<_Float16 *>(ws), batch, num_heads);
+        hipLaunchKernelGGL(out_proj_kernel<_Float16>, dim3(geo.grid), dim3(256), 0, s,
+                           reinterpret_cast<const _Float16 *>(ws), static_cast<const _Float16 *>(w_o),
+                           static_cast<_Float16 *>(out), part, batch, hv, d_model, geo);
+        if (split)
+            hipLaunchKernelGGL(reduce_units_kernel<_Float16>, dim3((quads + 255) / 256), dim3(256), 0, s, part,
+                               static_cast<_Float16 *>(out), batch, d_model, geo);
+    }
     const hipError_t e = hipPeekAtLastError();
     return e == hipSuccess ? MLA_STATUS_SUCCESS : record_hip_error(e);
 }
@@ -363,11 +486,15 @@ int project(bool bf16, const void *o_star, const void *w_uv, const void *w_o, vo
 
 extern "C" {
 
-size_t mla_project_output_workspace_size(int batch, int num_heads)
+size_t mla_project_output_workspace_size(int batch, int num_heads, int d_model)
 {
-    if (batch < 1 || num_heads < 1 || num_heads > 4096)
+    if (batch < 1 || num_heads < 1 || num_heads > 4096 || d_model < 1)
         return 0;
-    return ((size_t)batch * num_heads * mla::kNope * 2 + 255) / 256 * 256;
+    // the value projection [B x n_h*128] (16-bit), then the output
+    // projection's fp32 partial tiles (two per workgroup, at most kMaxGrid
+    // workgroups on any device)
+    const mla::OutProjGeom geo = mla::out_proj_geom(batch, num_heads * mla::kNope, d_model, mla::kMaxGrid);
+    return mla::align256((size_t)batch * num_heads * mla::kNope * 2) + (size_t)2 * geo.grid * mla::kPartTile * 4;
 }
 
 int mla_absorb_query_fp16(const void *q_nope, const void *q_rope, const void *w_uk, void *q_star, int batch,

@@ -25,6 +25,8 @@ thread_local int t_last_hip_error = 0;
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];
 
+}  // namespace
+
 // CUs of the current device (cached); 256 (MI355X) if it cannot be queried.
 int current_cu_count()
 {
@@ -39,6 +41,8 @@ int current_cu_count()
     g_cu_count[dev].store(n, std::memory_order_relaxed);
     return n;
 }
+
+namespace {
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 

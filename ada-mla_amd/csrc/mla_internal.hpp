@@ -80,6 +80,9 @@ struct Problem {
 // block, a stand-in for the operand conversions that lengthen its steps.
 enum class CacheKind { kPacked, kPaged, kF8 };
 
+// CUs of the current device (cached per device); 256 if it cannot be queried.
+int current_cu_count();
+
 // Records e as this host thread's last HIP error (mla_last_hip_error) and
 // returns MLA_STATUS_HIP_ERROR.
 int record_hip_error(hipError_t e);

@@ -258,7 +258,7 @@ class Runner:
             self.q_star = torch.empty(self.batch, n_h, 576, device=dev, dtype=dtype)
             self.o_star = torch.empty(self.batch, n_h, 512, device=dev, dtype=dtype)
             self.y = torch.empty(self.batch, d_model, device=dev, dtype=dtype)
-            self.pws_bytes = lib.mla_project_output_workspace_size(self.batch, n_h)
+            self.pws_bytes = lib.mla_project_output_workspace_size(self.batch, n_h, self.d_model)
             self.pws = torch.empty(self.pws_bytes, dtype=torch.uint8, device=dev)
 
         if partials == "auto":

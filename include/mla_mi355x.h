@@ -255,12 +255,13 @@ int mla_decode_split_batched_fp8(const void *query, const void *cache_fp8,
  * mla_project_output_*: o_star [batch][num_heads][512] (the decode's output)
  *   -> out [batch][d_model] = concat_h(o_star[:, h] W_UV[h]^T) W_O^T, with
  *   the per-head values in a caller workspace of
- *   mla_project_output_workspace_size(batch, num_heads) bytes.
+ *   mla_project_output_workspace_size(batch, num_heads, d_model) bytes
+ *   (the per-head values, then the output projection's fp32 K-part sums).
  * All three products are MFMA kernels of this library (fp32 accumulation)
  * and allocate nothing: W_UK and W_UV one workgroup per (head, column
- * slice), W_O streamed once from HBM through an LDS ring, 32 output columns
- * per workgroup. */
-size_t mla_project_output_workspace_size(int batch, int num_heads);
+ * slice), W_O streamed once from HBM through an LDS ring by at most one
+ * workgroup per CU, in K-parts whose fp32 sums a second small kernel adds. */
+size_t mla_project_output_workspace_size(int batch, int num_heads, int d_model);
 int mla_absorb_query_fp16(const void *q_nope, const void *q_rope,
                           const void *w_uk, void *q_star, int batch,
                           int num_heads, void *stream);

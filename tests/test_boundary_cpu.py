@@ -255,8 +255,15 @@ def test_block_projection_argument_errors():
         assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, 1, 16, 0, None) == capi.STATUS_INVALID_VALUE
         assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 16, 1, 16, 64, None) == capi.STATUS_WORKSPACE_TOO_SMALL
     # per-head values of B x n_h x 128 in the input dtype, 256-byte aligned
-    assert lib.mla_project_output_workspace_size(3, 16) == (3 * 16 * 128 * 2 + 255) // 256 * 256
-    assert lib.mla_project_output_workspace_size(0, 16) == 0
+    def a256(n):
+        return (n + 255) // 256 * 256
+    # the values, then two fp32 tiles of 32 x 64 per workgroup of the W_O kernel: 16 column blocks x
+    # 8 K-chunks = 128 steps, one per workgroup
+    assert lib.mla_project_output_workspace_size(3, 16, 1000) == a256(3 * 16 * 128 * 2) + 2 * 128 * 32 * 64 * 4
+    # at most 512 workgroups: 80 x 64 = 5120 steps
+    assert lib.mla_project_output_workspace_size(32, 128, 5120) == 32 * 128 * 128 * 2 + 2 * 512 * 32 * 64 * 4
+    assert lib.mla_project_output_workspace_size(0, 16, 1000) == 0
+    assert lib.mla_project_output_workspace_size(3, 16, 0) == 0
 
 
 def test_block_extension_rejects_bad_inputs():

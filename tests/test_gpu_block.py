@@ -26,7 +26,7 @@ def _rand(shape, seed, scale, dtype):
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float16, 1e-2), (torch.bfloat16, 3e-2)])
-@pytest.mark.parametrize("b,n_h", [(1, 16), (5, 128), (32, 16), (70, 32)])
+@pytest.mark.parametrize("b,n_h", [(1, 16), (5, 128), (32, 16), (70, 32), (2, 1), (3, 3)])
 def test_absorb_query(dtype, tol, b, n_h):
     print(f"absorb {dtype} B={b} n_h={n_h}", flush=True)
     qn, qn_d = _rand((b, n_h, 128), 1, 1.0, dtype)
@@ -42,7 +42,14 @@ def test_absorb_query(dtype, tol, b, n_h):
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float16, 1e-2), (torch.bfloat16, 3e-2)])
-@pytest.mark.parametrize("b,n_h,d_model", [(1, 16, 256), (4, 128, 5120), (33, 16, 1000), (70, 32, 512)])
+# The W_O kernel cuts its (64-column unit, K-chunk) steps into equal ranges,
+# one per workgroup; on a 256-CU MI355X: (32, 128, 5120), the block workload,
+# splits units between 3-4 workgroups; (33, 16, 1000) one unit over 8 (two
+# row groups); (256, 16, 8192) and (5, 1, 256) keep every unit in one
+# workgroup (direct stores, no reduction); n_h = 1 and 3 end K in a
+# 128-column chunk, (4, 3, 1000) with that chunk in a split unit.
+@pytest.mark.parametrize("b,n_h,d_model", [(1, 16, 256), (4, 128, 5120), (33, 16, 1000), (70, 32, 512),
+                                           (32, 128, 5120), (256, 16, 8192), (5, 1, 256), (4, 3, 1000)])
 def test_project_output(dtype, tol, b, n_h, d_model):
     print(f"project {dtype} B={b} n_h={n_h} d_model={d_model}", flush=True)
     o, o_d = _rand((b, n_h, 512), 4, 1.0, dtype)
