@@ -118,6 +118,25 @@ def test_bf16_batched_ragged_with_empty(splits):
             _check(got[b], ref[b], f"seq {b}")
 
 
+@pytest.mark.parametrize("n_h,splits", [(32, 1), (128, 2)])
+def test_bf16_batched_chunks_spanning_many_pieces(n_h, splits):
+    # chunks over three or more sequences: pieces of >= 4 blocks load their
+    # successor's Q* and first blocks during their last steps
+    seqlens = np.array([130, 200, 0, 150, 300, 129, 40, 260, 140, 0, 500, 97, 1000, 33, 160, 128, 1, 255])
+    q32, c32, cu = synthetic.batched_inputs(n_h, seqlens, seed=22, dtype=np.float32)
+    q = torch.from_numpy(q32).to(torch.bfloat16)
+    c = torch.from_numpy(c32).to(torch.bfloat16)
+    out = capi.decode_split_batched_bf16(q.cuda(), c.cuda(), torch.from_numpy(cu).cuda(), num_splits=splits)
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    ref = O.closed_form_batched(q.double().numpy(), c.double().numpy(), cu)
+    for b in range(len(seqlens)):
+        if seqlens[b] == 0:
+            assert not got[b].any()
+        else:
+            _check(got[b], ref[b], f"seq {b}")
+
+
 def test_bf16_extension_dispatch():
     import ada_mla
     q, c, _, _ = _bf16_inputs(128, 1500, seed=13)

@@ -85,6 +85,20 @@ def test_paged_long_sequences(page, dtype):
     _check_all(got, ref, n, 5e-3 if dtype == torch.float16 else 1e-2, f"long page={page}")
 
 
+# chunks spanning three or more sequences, with pieces that load their
+# successor's Q* and first blocks (>= 4 blocks) and pieces that do not
+MANY_PIECES = [130, 200, 0, 150, 300, 129, 40, 260, 140, 0, 500, 97, 1000, 33, 160, 128, 1, 255]
+
+
+@pytest.mark.parametrize("n_h", [16, 128])
+@pytest.mark.parametrize("page", [32, 64])
+@pytest.mark.parametrize("splits,dtype", [(1, torch.float16), (2, torch.float16), (3, torch.bfloat16)])
+def test_paged_chunks_spanning_many_pieces(n_h, page, splits, dtype):
+    print(f"paged many pieces n_h={n_h} page={page} splits={splits} {dtype}", flush=True)
+    got, ref, lens = _paged(n_h, np.array(MANY_PIECES), page, seed=23, dtype=dtype, splits=splits)
+    _check_all(got, ref, lens, 5e-3 if dtype == torch.float16 else 1e-2, f"paged many pieces {dtype}")
+
+
 def test_paged_config5_shape():
     seqlens = synthetic.batched_seqlens(32, seed=42)
     print(f"paged config 5 total={int(seqlens.sum())}", flush=True)

@@ -268,6 +268,42 @@ def test_batched_many_items_with_empty(n_h, batch, splits):
             _check16(got[b], ref[b], f"seq {b} N={seqlens[b]}")
 
 
+# Chunks that span three or more sequences (pieces). A piece of at least 4
+# blocks (128 tokens) with a successor loads the successor's Q* and first
+# blocks into the ring slots it frees in its last steps; shorter pieces leave
+# their successor to load its own; both kinds follow each other here, with
+# empty sequences between. Requested split counts fix the chunk length
+# (ceil(ceil(total / splits) / 32) * 32 tokens), so the test checks that it
+# covers what it claims.
+MANY_PIECES = np.array([130, 200, 0, 150, 300, 129, 40, 260, 140, 0, 500, 97, 1000, 33, 160, 128, 1, 255])
+
+
+def _max_pieces_per_chunk(seqlens, splits):
+    cu = np.concatenate([[0], np.cumsum(seqlens)])
+    total = int(cu[-1])
+    chunk = -(-(-(-total // splits)) // 32) * 32
+    most = 0
+    for lo in range(0, total, chunk):
+        hi = min(lo + chunk, total)
+        most = max(most, sum(1 for b in range(len(seqlens)) if max(cu[b], lo) < min(cu[b + 1], hi)))
+    return most
+
+
+@pytest.mark.parametrize("n_h", [16, 32, 64, 128])
+@pytest.mark.parametrize("splits", [1, 2, 3])
+def test_batched_chunks_spanning_many_pieces(n_h, splits):
+    assert _max_pieces_per_chunk(MANY_PIECES, splits) >= 3
+    print(f"many pieces n_h={n_h} splits={splits}", flush=True)
+    q, c, cu = synthetic.batched_inputs(n_h, MANY_PIECES, seed=21)
+    got = _batched(q, c, cu, num_splits=splits)
+    ref = O.closed_form_batched(q, c, cu)
+    for b, n in enumerate(MANY_PIECES):
+        if n == 0:
+            assert not got[b].any(), f"empty seq {b}"
+        else:
+            _check16(got[b], ref[b], f"seq {b} N={n}")
+
+
 def test_batched_equals_single_sequence_calls():
     seqlens = np.array([700, 129, 2048])
     q, c, cu = synthetic.batched_inputs(128, seqlens, seed=12)
