@@ -418,9 +418,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--spinup-ms", type=float, default=300.0,
+    ap.add_argument("--spinup-ms", type=float, default=1000.0,
                     help="untimed decode calls for at least this long before the warm-up steps, so that "
-                         "the GPU's clocks are at their steady state (a cold start reads up to 15%% slower)")
+                         "the GPU's clocks are at their steady state (a cold start reads up to 15%% slower; "
+                         "after 300 ms the first N = 4096 measurement of a process still read 12.4-12.9 "
+                         "instead of 11.8 us on some boxes)")
     ap.add_argument("--workload", default="n4096", choices=sorted(WORKLOADS))
     ap.add_argument("--num-splits", type=int, default=0)
     ap.add_argument("--partials", choices=("auto", "fp16", "fp32"), default="auto",
