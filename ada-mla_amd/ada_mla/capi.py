@@ -25,6 +25,7 @@ STATUS_SCRATCH_EXCEEDED = 5
 NOALLOC_SCRATCH_BYTES = 32 << 20
 FLAG_SCALAR_TRANSPOSE = 1
 FLAG_FP32_PARTIALS = 4
+FLAG_TWO_LAUNCHES = 8
 
 _vp, _i, _u, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint, ctypes.c_size_t
 _SIGNATURES = {
@@ -32,6 +33,7 @@ _SIGNATURES = {
     "mla_status_string": (ctypes.c_char_p, [_i]),
     "mla_last_hip_error": (_i, []),
     "mla_decode_split_num_splits": (_i, [_i, _i, _i, _u]),
+    "mla_decode_split_launches": (_i, [_i, _i, _i, _u]),
     "mla_decode_split_workspace_size": (_sz, [_i, _i, _i]),
     "mla_decode_split_fp16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "mla_decode_split_fp16_ex": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _u, _vp]),

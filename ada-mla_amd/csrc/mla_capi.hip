@@ -90,6 +90,10 @@ void set_chunks(Plan &p, int total_tokens, int batch, int w)
     p.xcd_remap = 1;
 }
 
+// Fixed cost (us) of a one-launch call (one chunk, the split kernel writes
+// the output): the two-launch fixed cost below less the combine launch.
+constexpr double kDirectFixedUs = 7.0;
+
 // Modelled time of one 16-bit decode call (us) for a plan, fitted to MI355X
 // measurements of this library (forced plans over head tile, split count and
 // partial precision): a fixed cost per call (two launches, the prologue, the
@@ -101,8 +105,13 @@ void set_chunks(Plan &p, int total_tokens, int batch, int w)
 // share a chunk but not an XCD (xcd_remap 0, which the planner no longer
 // produces) would re-read C from HBM; the model charges that as slower
 // steps.
-double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, int cu_count, bool paged)
+double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, int cu_count, bool paged,
+                   bool direct_ok)
 {
+    // one chunk of a single sequence: one launch, no partials, no combine
+    if (direct_ok && p.n_chunks == 1)
+        return kDirectFixedUs + (std::ceil((double)p.chunk / p.block_tokens) + 1.0) *
+                                    (p.head_tile == 64 ? 1.5 : p.head_tile == 32 ? 0.88 : 0.65);
     const double step_us = p.head_tile == 64 ? 1.5 : p.head_tile == 32 ? 0.88 : 0.65;
     const int wgs = p.n_chunks * p.n_head_tiles;
     const double rounds = std::ceil((double)wgs / cu_count);
@@ -174,7 +183,8 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
             w_lo = w_hi = num_splits;
         for (int w = w_lo; w <= w_hi; ++w) {
             set_chunks(c, total_tokens, batch, w);
-            const double us = modelled_us(c, num_heads, total_tokens, batch, cu_count, paged);
+            const double us = modelled_us(c, num_heads, total_tokens, batch, cu_count, paged,
+                                          batch == 1 && cache != CacheKind::kPaged);
             if (best_us == 0.0 || us < best_us) {
                 best = c;
                 best_us = us;
@@ -254,6 +264,16 @@ bool heads_ok(int num_heads) { return num_heads > 0 && num_heads % 16 == 0 && nu
 constexpr int kPhaseSplit = 1;
 constexpr int kPhaseCombine = 2;
 
+// Who merges the partials of a whole call (both phases) on plan p: with one
+// chunk, a single-sequence 16-bit call's split kernel writes the output
+// itself and the call is one launch; otherwise combine_kernel merges.
+int choose_merge(const Plan &p, bool single16, unsigned flags)
+{
+    if (!single16 || p.n_chunks != 1 || (flags & (MLA_FLAG_TWO_LAUNCHES | MLA_FLAG_SCALAR_TRANSPOSE)) != 0)
+        return kMergeCombine;
+    return kMergeDirect;
+}
+
 // Shared body of every entry point; `phases` selects the split kernel, the
 // combine, or both (in that order, on one stream).
 enum class Dtype { kF16, kBF16, kF32, kF8Cache };
@@ -275,9 +295,13 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
     const bool f32_part = !fp32 && !paging && dt != Dtype::kF8Cache && (flags & MLA_FLAG_FP32_PARTIALS) != 0;
     const CacheKind kind = paging != nullptr ? CacheKind::kPaged
                            : dt == Dtype::kF8Cache ? CacheKind::kF8 : CacheKind::kPacked;
-    const Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, current_cu_count(), kind, f32_part);
+    const int cu = current_cu_count();
+    Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, cu, kind, f32_part);
     if (workspace_bytes < partials_bytes(p, num_heads))
         return MLA_STATUS_WORKSPACE_TOO_SMALL;
+    const bool tr_load = (flags & MLA_FLAG_SCALAR_TRANSPOSE) == 0;
+    if (split && combine)
+        p.merge = choose_merge(p, batch == 1 && !fp32 && !paging, flags);
 
     Problem pb;
     pb.q = query;
@@ -297,12 +321,11 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
     hipStream_t s = static_cast<hipStream_t>(stream);
 
     if (split) {
-        const hipError_t e = fp32 ? launch_splitkv_fp32(pb, p, w, s)
-                                  : launch_splitkv_fp16(pb, p, w, (flags & MLA_FLAG_SCALAR_TRANSPOSE) == 0, s);
+        const hipError_t e = fp32 ? launch_splitkv_fp32(pb, p, w, s) : launch_splitkv_fp16(pb, p, w, tr_load, s);
         if (e != hipSuccess)
             return fail_hip(e);
     }
-    if (combine) {
+    if (combine && p.merge == kMergeCombine) {
         const hipError_t e = launch_combine(pb, p, w, s);
         if (e != hipSuccess)
             return fail_hip(e);
@@ -375,6 +398,15 @@ int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits, u
     return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
                           (flags & MLA_FLAG_FP32_PARTIALS) != 0)
         .n_chunks;
+}
+
+int mla_decode_split_launches(int num_heads, int seq_length, int num_splits, unsigned flags)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return 0;
+    const mla::Plan p = mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(),
+                                       mla::CacheKind::kPacked, (flags & MLA_FLAG_FP32_PARTIALS) != 0);
+    return mla::choose_merge(p, true, flags) == mla::kMergeCombine ? 2 : 1;
 }
 
 size_t mla_decode_split_workspace_size(int num_heads, int seq_length, int num_splits)

@@ -29,7 +29,12 @@ struct Plan {
                        // holds grid_chunks() chunks (n_chunks padded to a multiple of 8)
     int part_bytes;    // bytes per partial O element: 2 (16-bit paths), 4 (fp32 path, or 16-bit
                        // paths with fp32 partials)
+    int merge;         // kMergeCombine: combine_kernel merges the partials (a second launch);
+                       // kMergeDirect: one chunk, the split kernel writes the output itself
 };
+
+constexpr int kMergeCombine = 0;
+constexpr int kMergeDirect = 1;
 
 // Chunks in the split kernels' launch grid: with xcd_remap, workgroup b
 // takes chunk (b / 8 / n_head_tiles) * 8 + b % 8, so the grid is padded to a

@@ -103,7 +103,10 @@ struct F16Tile {
 // cache; the S and O waves convert their operands to fp16 after each LDS
 // read, exactly (every E4M3 value is an fp16 value). The per-tensor cache
 // scale is folded into scale_log2 and out_scale.
-template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part, bool kF8>
+// kDirect (one chunk of a single sequence, packed cache): the chunk's
+// normalised O is the output, so the O waves write it to out ([head][512])
+// and no partials, m or l are stored; the call needs no combine launch.
+template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part, bool kF8, bool kDirect>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void splitkv_fp16_kernel(const E *__restrict__ q,
                          const E *__restrict__ c,
@@ -113,7 +116,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                          float *__restrict__ l_part,
                          int num_heads, int batch, int total_tokens, int chunk,
                          int n_head_tiles, int xcd_remap, float scale_log2, Paging pg,
-                         float out_scale)
+                         float out_scale, E *__restrict__ out)
 {
     using T = F16Tile<HT>;
     static_assert(!(kF8 && (kPaged || !__is_same(E, _Float16))), "fp8 cache: packed layout, fp16 query");
@@ -543,7 +546,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 }
             }
             lds_barrier();
-            if (th == 0 && g == 0) {
+            if (!kDirect && th == 0 && g == 0) {
 #pragma unroll
                 for (int ns = 0; ns < T::kNS; ++ns) {
                     const int h = T::kSH * hg + 16 * ns + l16;
@@ -813,7 +816,11 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 // ---- epilogue: O of this piece normalised by its running sum
                 // (the halves' sums moved onto the reference max, exactly as
                 // the S waves compute the l they store), tile by tile
-                const size_t obase = (size_t)slot_out * num_heads * kDV + lane * 4;
+                // lane through an empty asm: the epilogue's addresses are formed
+                // here, not hoisted into registers held across the block loop
+                int eln = lane;
+                asm volatile("" : "+v"(eln));
+                const size_t obase = (size_t)slot_out * num_heads * kDV + eln * 4;
 #pragma unroll
                 for (int hs = 0; hs < T::kNHS; ++hs) {
                     const int h = 16 * hs + l16;
@@ -824,7 +831,11 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     for (int dt = 0; dt < 8; ++dt) {
                         const floatx4 v = o[hs][dt] * inv;
                         const size_t off = obase + frag_offset(head0 + 16 * hs, 128 * ow + 16 * dt);
-                        if constexpr (kF32Part) {
+                        if constexpr (kDirect) {
+                            // lane (g, h): dims 4g .. 4g+3 of head h of this 16-dim group
+                            E *const orow = out + (size_t)(head0 + 16 * hs + (eln & 15)) * kDV + 128 * ow + 4 * (eln >> 4);
+                            *(E4 *)(orow + 16 * dt) = E4{(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
+                        } else if constexpr (kF32Part) {
                             __builtin_nontemporal_store(v, (floatx4 *)((float *)o_part + off));
                         } else {
                             const E4 hv = {(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
@@ -876,28 +887,30 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             });
         }
     }
+
 }
 
-template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part = false, bool kF8 = false>
+template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part = false, bool kF8 = false, bool kDirect = false>
 hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStream_t s)
 {
     const dim3 grid(grid_chunks(p) * p.n_head_tiles), block(F16Tile<HT>::kThreads);
-    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part, kF8>), grid, block, 0, s,
+    hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part, kF8, kDirect>), grid, block, 0, s,
                        (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens, w.o, w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
-                       p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2, pb.paging, pb.out_scale);
+                       p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2, pb.paging, pb.out_scale,
+                       (E *)pb.out);
     // the launch's own error; hipPeekAtLastError leaves a sticky error from
     // the caller's earlier work in place for the caller to see
     return hipPeekAtLastError();
 }
 
-// one instantiation per head tile of a (cache type, partials) combination
-template <bool kTr, typename E, bool kPaged, bool kF32Part, bool kF8>
+// one instantiation per head tile of a (cache type, partials, output) combination
+template <bool kTr, typename E, bool kPaged, bool kF32Part, bool kF8, bool kDirect = false>
 hipError_t launch_tiles(const Problem &pb, const Plan &p, const Partials &w, hipStream_t s)
 {
     switch (p.head_tile) {
-    case 64: return launch_ht<64, kTr, E, kPaged, kF32Part, kF8>(pb, p, w, s);
-    case 32: return launch_ht<32, kTr, E, kPaged, kF32Part, kF8>(pb, p, w, s);
-    case 16: return launch_ht<16, kTr, E, kPaged, kF32Part, kF8>(pb, p, w, s);
+    case 64: return launch_ht<64, kTr, E, kPaged, kF32Part, kF8, kDirect>(pb, p, w, s);
+    case 32: return launch_ht<32, kTr, E, kPaged, kF32Part, kF8, kDirect>(pb, p, w, s);
+    case 16: return launch_ht<16, kTr, E, kPaged, kF32Part, kF8, kDirect>(pb, p, w, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -910,6 +923,16 @@ hipError_t launch_splitkv_fp16(const Problem &pb, const Plan &p, const Partials 
     if (p.n_chunks == 0)
         return hipSuccess;
     const bool f32_part = p.part_bytes == 4;
+    if (p.merge == kMergeDirect) {
+        // one chunk of a single sequence, packed cache: the output directly
+        // (the partial precision does not matter: none are stored)
+        if (!tr_load || pb.paging.block_table || pb.batch != 1 || p.n_chunks != 1 || !pb.out)
+            return hipErrorInvalidValue;
+        if (pb.fp8)
+            return launch_tiles<true, _Float16, false, false, true, true>(pb, p, w, s);
+        return pb.bf16 ? launch_tiles<true, __bf16, false, false, false, true>(pb, p, w, s)
+                       : launch_tiles<true, _Float16, false, false, false, true>(pb, p, w, s);
+    }
     // The scalar transpose reads and fp32 partials are options of the packed
     // fp16 entry points (their flags); the bf16, paged and fp8 caches are
     // built with the LDS transpose read and 16-bit partials only.

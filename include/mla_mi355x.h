@@ -62,6 +62,15 @@ extern "C" {
  * queries cover both precisions. */
 #define MLA_FLAG_FP32_PARTIALS 4u
 
+/* A single-sequence 16-bit call (mla_decode_split_fp16/_ex, _bf16, _fp8 and
+ * the allocation-free entry point) whose plan has one split is ONE launch:
+ * the split kernel writes the output itself, with no partials and no
+ * combine (the planner prefers one split for short sequences, about
+ * 200 tokens or fewer at 128 heads, for that reason). This flag keeps the
+ * reference's two launches in that case too: split kernel, then the LSE
+ * combine (csrc/mla_decode_splitk_fwd.cuh:973-978). */
+#define MLA_FLAG_TWO_LAUNCHES 8u
+
 int mla_abi_version(void);
 const char *mla_status_string(int status);
 /* hipError_t of the last failed HIP call on this thread (0 if none). */
@@ -74,6 +83,13 @@ int mla_last_hip_error(void);
  * (csrc/mla_api.cpp:97). */
 int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits,
                                 unsigned flags);
+
+/* Kernel launches (1 or 2, see MLA_FLAG_TWO_LAUNCHES) that
+ * mla_decode_split_fp16_ex makes for these arguments and flags on the
+ * current device; 0 for invalid sizes. No counterpart in the reference, whose
+ * launcher always makes two (csrc/mla_decode_splitk_fwd.cuh:973-978). */
+int mla_decode_split_launches(int num_heads, int seq_length, int num_splits,
+                              unsigned flags);
 
 /* Workspace for mla_decode_split_fp16 (split partials: O normalised by its
  * running sum in fp16, running max and sum in fp32). Replaces the

@@ -242,6 +242,22 @@ def test_plan_cache_returns_the_same_plans():
     assert lib.mla_decode_split_num_splits(128, 65536, 0, 0) != lib.mla_decode_split_num_splits(128, 65536, 0, 4)
 
 
+def test_single_launch_choice():
+    # a whole single-sequence call whose plan has one split is one launch;
+    # the flags that select the two-launch path are honoured
+    lib = capi.load()
+    f = lib.mla_decode_split_launches
+    for n_h, n in [(128, 1), (128, 32), (128, 128), (16, 100), (64, 200)]:
+        assert lib.mla_decode_split_num_splits(n_h, n, 0, 0) == 1, (n_h, n)
+        assert f(n_h, n, 0, 0) == 1, (n_h, n)
+        assert f(n_h, n, 0, capi.FLAG_TWO_LAUNCHES) == 2
+        assert f(n_h, n, 0, capi.FLAG_SCALAR_TRANSPOSE) == 2
+    for n_h, n in [(128, 4096), (16, 32768), (128, 65536)]:
+        assert f(n_h, n, 0, 0) == 2
+    assert f(128, 4096, 1, 0) == 1  # a requested single split
+    assert f(24, 100, 0, 0) == 0 and f(128, 0, 0, 0) == 0
+
+
 def test_block_projection_argument_errors():
     lib = capi.load()
     for fn in ("mla_absorb_query_fp16", "mla_absorb_query_bf16"):

@@ -130,9 +130,10 @@ def test_fp32_matches_c_restatement_of_reference_cpu_kernel():
 
 def test_transpose_read_equals_scalar_read():
     # the two ways of reading C_N^T feed identical MFMA operands
+    # (the scalar read is built for the two-launch path only)
     for n_h, n in [(16, 200), (128, 1000), (32, 77)]:
         q, c = synthetic.decode_inputs(n_h, n, seed=n)
-        a = _fp16(q, c)
+        a = _fp16(q, c, flags=capi.FLAG_TWO_LAUNCHES)
         b = _fp16(q, c, flags=capi.FLAG_SCALAR_TRANSPOSE)
         assert np.array_equal(a, b), (n_h, n)
 
@@ -406,10 +407,11 @@ def test_config3_n65536_fp32_partials():
 
 @pytest.mark.parametrize("flags", [0, 4])
 def test_two_phase_api_equals_single_call(flags):
+    # the two phases are the two-launch call's launches
     lib = capi.load()
     q, c = synthetic.decode_inputs(128, 3000, seed=21)
     qt, ct = _t(q), _t(c)
-    one = capi.decode_split_fp16(qt, ct, flags=flags)
+    one = capi.decode_split_fp16(qt, ct, flags=flags | capi.FLAG_TWO_LAUNCHES)
     out = torch.empty_like(one)
     ws_bytes = lib.mla_decode_split_workspace_size(128, 3000, 0)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qt.device)
