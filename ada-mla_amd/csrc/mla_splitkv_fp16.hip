@@ -115,14 +115,18 @@ constexpr int kModeDirect = 2;
 
 template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part, bool kF8, int kMode>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+// Arguments: what the workgroup mapping and a single sequence's entry loads
+// need come first, within the 16 dwords preloaded into SGPRs at wave launch
+// (the library is built with -amdgpu-kernarg-preload-count=16).
 void splitkv_fp16_kernel(const E *__restrict__ q,
                          const E *__restrict__ c,
                          const int *__restrict__ cu_seqlens,
+                         int num_heads, int batch, int total_tokens, int chunk,
+                         int n_head_tiles, int xcd_remap,
                          void *__restrict__ o_part,
                          float *__restrict__ m_part,
                          float *__restrict__ l_part,
-                         int num_heads, int batch, int total_tokens, int chunk,
-                         int n_head_tiles, int xcd_remap, float scale_log2, Paging pg,
+                         float scale_log2, Paging pg,
                          float out_scale, E *__restrict__ out)
 {
     using T = F16Tile<HT>;
@@ -924,8 +928,8 @@ hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStr
 {
     const dim3 grid(grid_chunks(p) * p.n_head_tiles), block(F16Tile<HT>::kThreads);
     hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part, kF8, kMode>), grid, block, 0, s,
-                       (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens, w.o, w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
-                       p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2, pb.paging, pb.out_scale,
+                       (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens, pb.num_heads, pb.batch, pb.total_tokens,
+                       p.chunk, p.n_head_tiles, p.xcd_remap, w.o, w.m, w.l, pb.scale_log2, pb.paging, pb.out_scale,
                        (E *)pb.out);
     // the launch's own error; hipPeekAtLastError leaves a sticky error from
     // the caller's earlier work in place for the caller to see
