@@ -67,7 +67,7 @@ void combine_kernel(const PartT *__restrict__ o_part,
                     const float *__restrict__ l_part,
                     const int *__restrict__ cu_seqlens,
                     void *__restrict__ out,
-                    int num_heads, int total_tokens, int chunk, int n_items)
+                    int num_heads, int total_tokens, int chunk, int n_items, int n_chunks)
 {
     constexpr int kWaves = W > 8 ? W : 8;
     constexpr int kItems = kWaves / W;
@@ -79,26 +79,36 @@ void combine_kernel(const PartT *__restrict__ o_part,
     __shared__ floatx4 s_o[W > 1 ? kWaves : 1][64];
 
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    // wave-uniform values live in SGPRs: the index arithmetic (divisions
+    // included) runs once per wave on the scalar unit, ahead of the loads
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int item = blockIdx.x * kItems + w / W;
     const int k = w % W;  // this wave's place among the item's W waves
-    const int n_tiles = num_heads / 16 * (kDV / 16);
     const bool valid = item < n_items;
-    const int tile = valid ? item % n_tiles : 0;  // (head / 16) * 32 + dim / 16
-    const int b = valid ? item / n_tiles : 0;
+    // one sequence (no cu_seqlens): the item is the tile and the slots are
+    // the n_chunks chunks, with no division; a batch: (sequence, tile) and
+    // the sequence's slot range from its token range
+    int tile = 0, b = 0, s0 = 0, ns = 0;
+    if (!cu_seqlens) {
+        tile = item;
+        ns = valid ? n_chunks : 0;
+    } else if (valid) {
+        const int n_tiles = num_heads / 16 * (kDV / 16);
+        tile = item % n_tiles;  // (head / 16) * 32 + dim / 16
+        b = item / n_tiles;
+        const int lo = min(max(cu_seqlens[b], 0), total_tokens);
+        const int hi = min(max(cu_seqlens[b + 1], lo), total_tokens);
+        if (hi > lo) {
+            s0 = lo / chunk + b;
+            ns = (hi - 1) / chunk + b - s0 + 1;
+        }
+    }
     const int head = (tile >> 5) * 16 + (lane & 15);
     const int dim0 = (tile & 31) * 16 + 4 * (lane >> 4);
 
-    int lo = 0, hi = valid ? total_tokens : 0;
-    if (valid && cu_seqlens) {
-        lo = min(max(cu_seqlens[b], 0), total_tokens);
-        hi = min(max(cu_seqlens[b + 1], lo), total_tokens);
-    }
     float m = -INFINITY, l = 0.f;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (hi > lo) {  // uniform per wave
-        const int s0 = lo / chunk + b;
-        const int ns = (hi - 1) / chunk + b - s0 + 1;
+    if (ns > 0) {  // uniform per wave
         const size_t slot_elems = (size_t)num_heads * kDV;
         const PartT *op = o_part + (size_t)s0 * slot_elems + (size_t)tile * 256 + lane * 4;
         const float *mp = m_part + (size_t)s0 * num_heads + head;
@@ -223,7 +233,8 @@ void combine_tiles_kernel(const PartT *__restrict__ o_part,
         float l[kUT];
     };
     const int lane = threadIdx.x & 63;
-    const int grp = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // wave-uniform: the group's index arithmetic runs on the scalar unit
+    const int grp = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (grp >= n_groups)  // uniform per wave; no barriers follow
         return;
     constexpr int kGroupsPerHeads = kDV / 16 / kT;  // tile groups per 16 heads
@@ -335,7 +346,7 @@ void launch_w(const Problem &pb, const Plan &p, const Partials &w, int n_items, 
     constexpr int kItems = kWaves / W;
     hipLaunchKernelGGL((combine_kernel<PartT, OutT, W>), dim3((n_items + kItems - 1) / kItems),
                        dim3(64 * kWaves), 0, s, static_cast<const PartT *>(w.o), w.m, w.l,
-                       pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk, n_items);
+                       pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk, n_items, p.n_chunks);
 }
 
 template <typename PartT, typename OutT>
