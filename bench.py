@@ -28,7 +28,8 @@ Prints ONE JSON line. With the default workload the line also carries
 `other_configs`: BASELINE configs 3, 4 and 5 (N = 65536 with fp32 partials,
 n_h = 16, batched B = 32) measured the same way in the same run. --workload
 picks another configuration (n65536, nh16, batched, paged, block, bf16, the fp8
-cache workloads, fp32 and fp32_n4096) as the main line.
+cache workloads, fp32, fp32_n4096 and n256, a short sequence on the one-launch
+path) as the main line.
 """
 from __future__ import annotations
 
@@ -59,6 +60,8 @@ WORKLOADS = {
     "n4096": dict(kind="fp16", n_h=128, n=4096, desc="fp16 single sequence, n_h=128, N=4096 (BASELINE config 2)"),
     "n65536": dict(kind="fp16", n_h=128, n=65536, desc="fp16 split-KV, n_h=128, N=65536 (BASELINE config 3)"),
     "nh16": dict(kind="fp16", n_h=16, n=32768, desc="fp16 low-head, n_h=16, N=32768 (BASELINE config 4)"),
+    "n256": dict(kind="fp16", n_h=128, n=256, desc="fp16 short sequence, n_h=128, N=256 (one split: the one-launch "
+                                                  "path, no combine)"),
     "batched": dict(kind="batched", n_h=128, batch=32,
                     desc="fp16 batched, B=32, N_b ~ U[512,16384] seed 42 (BASELINE config 5)"),
     "fp32": dict(kind="fp32", n_h=128, n=1024, desc="fp32 path, n_h=128, N=1024 (BASELINE config 1 shape on GPU)"),
