@@ -79,4 +79,19 @@ __device__ __forceinline__ void global_to_lds16(const void *base, int off, const
                  : "=&s"(saved_m0) : "v"(off), "s"(base), "s"(l) : "memory");
 }
 
+// The same load with the LDS destination given as a wave-uniform LDS byte
+// address, for the steady-state feeding: its lane offsets are formed once and
+// kept in registers of their own. Offsets recomputed into one shared register
+// before every load made each load's address arithmetic wait until the
+// previous load had read that register.
+__device__ __forceinline__ void global_to_lds16_at(const void *base, int off, unsigned lds_addr)
+{
+    unsigned saved_m0;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %3\n\t"
+                 "global_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved_m0) : "v"(off), "s"(base), "s"(lds_addr) : "memory");
+}
+
 }  // namespace mla

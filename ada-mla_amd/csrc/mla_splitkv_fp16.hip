@@ -137,7 +137,11 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     using E4 = typename Vec<E>::v4;
     __shared__ __attribute__((aligned(1024))) E s_ring[T::kRing * T::kSlot];
     __shared__ __attribute__((aligned(16))) E s_p[2][HT * T::kPRow];
-    __shared__ float s_m[2][2][HT];  // [P buffer][token half][head]: running max of the half
+    // [P buffer][head % 16][head / 16][token half]: running max of the half,
+    // so that an O wave reads the maxima of all its heads (both halves) with
+    // one or two 16-byte reads per lane; m_at(h, th) indexes a buffer
+    __shared__ __attribute__((aligned(16))) float s_m[2][2 * HT];
+    auto m_at = [](int h, int th) { return ((h & 15) * T::kNHS + (h >> 4)) * 2 + th; };
     __shared__ float s_l[2][HT];     // [token half][head]: running sum at the end of a piece
     __shared__ float s_mref[HT];     // [head]: the O accumulators' reference max at the end of a piece
 
@@ -229,6 +233,28 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         const int rrow = 8 * ru + (ln >> 3);
         global_to_lds16(base, min(rrow, lim) * (kDK * 2) + 2 * (kDV + 8 * ((ln & 7) ^ rope_swizzle(rrow))),
                         s_ring + slot * T::kSlot + T::kRope + 512 * ru);
+    };
+    // Steady-state ring feeding: the lane part of a unit's global offset is
+    // the same for every block, so each feeder forms it once (feed_off) and
+    // a load then takes the block's first-row address (the row of a C_N
+    // unit added to it, clamped to `lim`, on the scalar unit), that offset
+    // and the slot's LDS address. A block cut short by the end of a piece
+    // (lim < 31) loads its rope rows through dma_rope, which clamps per lane.
+    const unsigned ring_lds = (unsigned)(uintptr_t)(const MLA_LDS E *)s_ring;
+    auto feed_off = [&](int row_or_ru, bool rope) -> int {
+        if (!rope)
+            return 16 * (lane ^ row_swizzle(row_or_ru));
+        const int r = lane >> 3;  // row within the unit's 8
+        return r * (kDK * 2) + 2 * (kDV + 8 * ((lane & 7) ^ rope_swizzle(8 * row_or_ru + r)));
+    };
+    auto feed_row = [&](const E *base, int lim, int slot, int row, int off) {
+        global_to_lds16_at(base + (size_t)min(row, lim) * kDK, off, ring_lds + 2 * (slot * T::kSlot + row * kDV));
+    };
+    auto feed_rope = [&](const E *base, int lim, int slot, int ru, int off) {
+        if (lim >= 8 * ru + 7)
+            global_to_lds16_at(base + (size_t)8 * ru * kDK, off, ring_lds + 2 * (slot * T::kSlot + T::kRope + 512 * ru));
+        else
+            dma_rope(base, lim, slot, ru);
     };
     // Global address of token t0 of sequence b (first token seq_lo), in two
     // steps so that a paged cache's block-table read can be issued early:
@@ -563,7 +589,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                             *(E2 *)(pw + 4) = E2{ph[1], ph[3]};
                         }
                         if (g == 0)
-                            s_m[blk & 1][th][hrow] = mn;
+                            s_m[blk & 1][m_at(hrow, th)] = mn;
                     }
                 }
                 if (t + 2 < T::kPre)
@@ -576,7 +602,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             for (int ns = 0; ns < T::kNS; ++ns) {
                 const float ls = sum_over_lane_groups(l_lane[ns]);
                 if (g == 0) {
-                    s_m[0][th][T::kSH * hg + 16 * ns + l16] = m_run[ns];
+                    s_m[0][m_at(T::kSH * hg + 16 * ns + l16, th)] = m_run[ns];
                     s_l[th][T::kSH * hg + 16 * ns + l16] = ls;
                 }
             }
@@ -589,7 +615,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     // most kLazyRescale below the halves' maxima), so that m, l
                     // and O share one scale
                     const float mr = s_mref[h];
-                    const float ls = s_l[0][h] * fast_exp2(s_m[0][0][h] - mr) + s_l[1][h] * fast_exp2(s_m[0][1][h] - mr);
+                    const float ls = s_l[0][h] * fast_exp2(s_m[0][m_at(h, 0)] - mr) + s_l[1][h] * fast_exp2(s_m[0][m_at(h, 1)] - mr);
                     __builtin_nontemporal_store(mr, m_part + (size_t)slot_out * num_heads + head0 + h);
                     __builtin_nontemporal_store(ls, l_part + (size_t)slot_out * num_heads + head0 + h);
                 }
@@ -611,7 +637,15 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         constexpr int kFU = kFeedPairs ? T::kFeedRows / 2 + 1 : T::kFeedUnits;  // units per feeder and block
         static_assert(!kFeedPairs || T::kFeedRows == 16 || T::kFeedRows == 8, "paired fp8 units");
         // unit k (0..kFeedUnits-1) of this feeder's share of a block: C_N
-        // row kFeedRows*feeder + k, or a rope unit of those rows
+        // row kFeedRows*feeder + k, or a rope unit of those rows; uoff[k] is
+        // its lane offset (16-bit caches)
+        int uoff[kFeedPairs ? 1 : kFU];
+        if constexpr (!kF8) {
+#pragma unroll
+            for (int k = 0; k < kFU; ++k)
+                uoff[k] = k < T::kFeedRows ? feed_off(T::kFeedRows * feeder + k, false)
+                                           : feed_off((T::kFeedRows / 8) * feeder + (k - T::kFeedRows), true);
+        }
         auto load_unit = [&](const void *base, int lim, int slot, int k) {
             if constexpr (kFeedPairs) {
                 // fp8, dedicated feeders: row pairs, then one 16-row rope unit
@@ -623,10 +657,17 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         dma_rope8x16(b8, lim, slot, feeder);
                     else
                         dma_rope8(b8, lim, slot, feeder);
-            } else if (k < T::kFeedRows) {
-                blk_row(base, lim, slot, T::kFeedRows * feeder + k);
+            } else if constexpr (kF8) {
+                if (k < T::kFeedRows)
+                    blk_row(base, lim, slot, T::kFeedRows * feeder + k);
+                else
+                    blk_rope(base, lim, slot, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
             } else {
-                blk_rope(base, lim, slot, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows));
+                const E *eb = static_cast<const E *>(base);
+                if (k < T::kFeedRows)
+                    feed_row(eb, lim, slot, T::kFeedRows * feeder + k, uoff[k]);
+                else
+                    feed_rope(eb, lim, slot, (T::kFeedRows / 8) * feeder + (k - T::kFeedRows), uoff[k]);
             }
         };
         // End of step t: block t+2 (the S waves' next) must have landed;
@@ -765,12 +806,26 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         // 2^(M_old - M)
                         E8 pb[T::kNHS];
                         float m0[T::kNHS], m1[T::kNHS];
+                        {
+                            const float *mrow = s_m[blk & 1] + m_at(l16, 0);
+                            if constexpr (T::kNHS == 1) {
+                                const float2 v = *(const float2 *)mrow;
+                                m0[0] = v.x;
+                                m1[0] = v.y;
+                            } else {
 #pragma unroll
-                        for (int hs = 0; hs < T::kNHS; ++hs) {
-                            m0[hs] = s_m[blk & 1][0][16 * hs + l16];
-                            m1[hs] = s_m[blk & 1][1][16 * hs + l16];
-                            pb[hs] = *(const E8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
+                                for (int q = 0; q < T::kNHS / 2; ++q) {
+                                    const floatx4 v = *(const floatx4 *)(mrow + 4 * q);
+                                    m0[2 * q] = v[0];
+                                    m1[2 * q] = v[1];
+                                    m0[2 * q + 1] = v[2];
+                                    m1[2 * q + 1] = v[3];
+                                }
+                            }
                         }
+#pragma unroll
+                        for (int hs = 0; hs < T::kNHS; ++hs)
+                            pb[hs] = *(const E8 *)(s_p[blk & 1] + (16 * hs + l16) * T::kPRow + 8 * g);
                         // The reference only moves when a max passes it by more
                         // than kLazyRescale (P scaled onto it then stays <= 2^8,
                         // well inside fp16), so the rescale is rare.
@@ -858,8 +913,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
 #pragma unroll
                 for (int hs = 0; hs < T::kNHS; ++hs) {
                     const int h = 16 * hs + l16;
-                    const float ls = s_l[0][h] * fast_exp2(s_m[0][0][h] - m_ref[hs]) +
-                                     s_l[1][h] * fast_exp2(s_m[0][1][h] - m_ref[hs]);
+                    const float ls = s_l[0][h] * fast_exp2(s_m[0][m_at(h, 0)] - m_ref[hs]) +
+                                     s_l[1][h] * fast_exp2(s_m[0][m_at(h, 1)] - m_ref[hs]);
                     const float inv = out_scale / ls;
 #pragma unroll
                     for (int dt = 0; dt < 8; ++dt) {
