@@ -520,6 +520,14 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     };
                     load_batch(0, 0);
                     load_batch(1, kB);
+                    // fp8: each K-step's operand is converted one K-step
+                    // ahead, into the other of two register sets, so that
+                    // the conversions run while the previous MFMAs do (one
+                    // set made every conversion wait for the MFMAs before it
+                    // to read their operand, and every MFMA for its operand)
+                    E8 cv[2];
+                    if constexpr (kF8)
+                        cv[0] = f8_to_f16(ab[0][0]);
 #pragma unroll
                     for (int bi = 0; bi < kNB; ++bi) {
                         if (bi + 2 < kNB)
@@ -528,10 +536,14 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
 #pragma unroll
                         for (int k = 0; k < kB; ++k) {
                             E8 a;
-                            if constexpr (kF8)
-                                a = f8_to_f16(ab[bi % 3][k]);
-                            else
+                            if constexpr (kF8) {
+                                const int j = bi * kB + k;  // K-step
+                                a = cv[j & 1];
+                                if (j + 1 < kDK / 32)
+                                    cv[(j + 1) & 1] = f8_to_f16(ab[((j + 1) / kB) % 3][(j + 1) % kB]);
+                            } else {
                                 a = ab[bi % 3][k];
+                            }
 #pragma unroll
                             for (int ns = 0; ns < T::kNS; ++ns) {
                                 const int kk = bi * kB + k;
@@ -868,13 +880,21 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         // waves feed, this step's global->LDS loads) placed
                         // between the MFMAs
                         const E *cn = s_ring + ((blk + 1) % T::kRing) * T::kSlot;
+                        // fp8: operands converted one dim tile ahead, into two
+                        // register sets (as in the S waves)
+                        E8 cva[2];
+                        if constexpr (kF8)
+                            cva[0] = f8_to_f16(av[0]);
 #pragma unroll
                         for (int dt = 0; dt < 8; ++dt) {
                             E8 a;
-                            if constexpr (kF8)
-                                a = f8_to_f16(av[dt]);
-                            else
+                            if constexpr (kF8) {
+                                a = cva[dt & 1];
+                                if (dt + 1 < 8)
+                                    cva[(dt + 1) & 1] = f8_to_f16(av[dt + 1]);
+                            } else {
                                 a = av[dt];
+                            }
 #pragma unroll
                             for (int hs = 0; hs < T::kNHS; ++hs)
                                 o[hs][dt] = mfma16x16x32(a, pb[hs], o[hs][dt]);
