@@ -274,6 +274,18 @@ int choose_merge(const Plan &p, bool single16, unsigned flags)
     return kMergeDirect;
 }
 
+// How the 16-bit split kernel stores its partials. Nontemporal stores keep
+// them out of the L2, which the kernel's end then need not write back (N =
+// 4096: 12.78 -> 11.85 us per call when introduced). A combine of only a
+// few workgroups is instead bound by each CU's read latency, and reads plain
+// stored partials faster. Same box, plain against nontemporal: n_h = 16
+// (32 combine workgroups) 15.55 -> 14.80 us; N = 4096 (256) 10.77 -> 11.01 us,
+// N = 65536 with fp32 partials (256) 37.4 -> 38.3 us, batched (512) 94.2 -> 93.5.
+int choose_part_plain(const Plan &p, int batch, int num_heads, int cu_count)
+{
+    return 4 * combine_workgroups(p, batch, num_heads) < cu_count ? 1 : 0;
+}
+
 // Shared body of every entry point; `phases` selects the split kernel, the
 // combine, or both (in that order, on one stream).
 enum class Dtype { kF16, kBF16, kF32, kF8Cache };
@@ -302,6 +314,7 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
     const bool tr_load = (flags & MLA_FLAG_SCALAR_TRANSPOSE) == 0;
     if (split && combine)
         p.merge = choose_merge(p, batch == 1 && !fp32 && !paging, flags);
+    p.part_plain = choose_part_plain(p, batch, num_heads, cu);
 
     Problem pb;
     pb.q = query;

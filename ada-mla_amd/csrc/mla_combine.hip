@@ -391,6 +391,16 @@ int combine_waves_per_item(const Plan &p, int batch, int n_items)
     return waves;
 }
 
+int combine_workgroups(const Plan &p, int batch, int num_heads)
+{
+    const int n_items = num_heads / 16 * (kDV / 16) * batch;
+    const int waves = combine_waves_per_item(p, batch, n_items);
+    if (waves == 0)
+        return (n_items / kT + 3) / 4;
+    const int items_per_wg = (waves > 8 ? waves : 8) / waves;
+    return (n_items + items_per_wg - 1) / items_per_wg;
+}
+
 hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
                           hipStream_t s)
 {

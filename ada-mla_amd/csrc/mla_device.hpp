@@ -107,6 +107,27 @@ __device__ __forceinline__ float sum_over_lane_groups(float v)
     return reduce_over_lane_groups(v, [](float x, float y) { return x + y; });
 }
 
+// Global stores with the nontemporal bit, as inline asm: a store the
+// compiler knows (__builtin_nontemporal_store) that sits in one branch of a
+// runtime choice is merged with a plain store of the same value and address
+// in the other branch, and the hint is dropped. No memory clobber: they are
+// for results that nothing in the storing kernel reads back, so other
+// accesses may move across them.
+__device__ __forceinline__ void store_nt(float *p, float v)
+{
+    asm volatile("global_store_dword %0, %1, off nt" ::"v"(p), "v"(v));
+}
+__device__ __forceinline__ void store_nt(floatx4 *p, floatx4 v)
+{
+    asm volatile("global_store_dwordx4 %0, %1, off nt" ::"v"(p), "v"(v));
+}
+template <typename V4>  // 4 x 16-bit elements
+__device__ __forceinline__ void store_nt8(V4 *p, V4 v)
+{
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    asm volatile("global_store_dwordx2 %0, %1, off nt" ::"v"(p), "v"(__builtin_bit_cast(u32x2, v)));
+}
+
 // Offset (in floats) of O[head][dim] within one slot of the fp32 partial
 // output: 16 x 16 tiles (16 heads x 16 value dims) stored in the MFMA
 // accumulator order, lane (16 * g + head % 16) holding dims 4g .. 4g+3 of

@@ -31,6 +31,8 @@ struct Plan {
                        // paths with fp32 partials)
     int merge;         // kMergeCombine: combine_kernel merges the partials (a second launch);
                        // kMergeDirect: one chunk, the split kernel writes the output itself
+    int part_plain;    // 1: the 16-bit split kernel stores its partials with plain stores,
+                       // 0: with nontemporal ones (see choose_part_plain)
 };
 
 constexpr int kMergeCombine = 0;
@@ -104,6 +106,9 @@ hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p,
                                const Partials &w, hipStream_t s);
 // The output has the partials' type: fp16 / bf16 on the 16-bit path, fp32
 // on the fp32 path.
+// Workgroups of the combine launch for plan p (batch sequences, num_heads).
+int combine_workgroups(const Plan &p, int batch, int num_heads);
+
 hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
                           hipStream_t s);
 

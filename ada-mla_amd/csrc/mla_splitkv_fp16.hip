@@ -52,7 +52,9 @@
 //    The partials (O, m, l) are written with nontemporal stores: they are read
 //    once, by the combine kernel, and kept out of the L2 they need not be
 //    written back from at the end of the kernel. Measured at N = 4096 (4.2 MB
-//    of partials): 12.78 -> 11.85 us per call.
+//    of partials): 12.78 -> 11.85 us per call. Plans whose combine runs on
+//    few workgroups store them plainly instead (part_plain; the planner's
+//    choose_part_plain has the measurements).
 #include <type_traits>
 
 #include "mla_device.hpp"
@@ -127,7 +129,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                          float *__restrict__ m_part,
                          float *__restrict__ l_part,
                          float scale_log2, Paging pg,
-                         float out_scale, E *__restrict__ out)
+                         float out_scale, E *__restrict__ out, int part_plain)
 {
     using T = F16Tile<HT>;
     constexpr bool kDirect = kMode == kModeDirect;
@@ -628,8 +630,15 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     // and O share one scale
                     const float mr = s_mref[h];
                     const float ls = s_l[0][h] * fast_exp2(s_m[0][m_at(h, 0)] - mr) + s_l[1][h] * fast_exp2(s_m[0][m_at(h, 1)] - mr);
-                    __builtin_nontemporal_store(mr, m_part + (size_t)slot_out * num_heads + head0 + h);
-                    __builtin_nontemporal_store(ls, l_part + (size_t)slot_out * num_heads + head0 + h);
+                    float *const mp = m_part + (size_t)slot_out * num_heads + head0 + h;
+                    float *const lp = l_part + (size_t)slot_out * num_heads + head0 + h;
+                    if (part_plain) {
+                        *mp = mr;
+                        *lp = ls;
+                    } else {
+                        store_nt(mp, mr);
+                        store_nt(lp, ls);
+                    }
                 }
             }
         });
@@ -945,10 +954,18 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                             E *const orow = out + (size_t)(head0 + 16 * hs + (eln & 15)) * kDV + 128 * ow + 4 * (eln >> 4);
                             *(E4 *)(orow + 16 * dt) = E4{(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
                         } else if constexpr (kF32Part) {
-                            __builtin_nontemporal_store(v, (floatx4 *)((float *)o_part + off));
+                            floatx4 *const op = (floatx4 *)((float *)o_part + off);
+                            if (part_plain)
+                                *op = v;
+                            else
+                                store_nt(op, v);
                         } else {
                             const E4 hv = {(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
-                            __builtin_nontemporal_store(hv, (E4 *)((E *)o_part + off));
+                            E4 *const op = (E4 *)((E *)o_part + off);
+                            if (part_plain)
+                                *op = hv;
+                            else
+                                store_nt8(op, hv);
                         }
                     }
                 }
@@ -1005,7 +1022,7 @@ hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStr
     hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part, kF8, kMode>), grid, block, 0, s,
                        (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, w.o, w.m, w.l, pb.scale_log2, pb.paging, pb.out_scale,
-                       (E *)pb.out);
+                       (E *)pb.out, p.part_plain);
     // the launch's own error; hipPeekAtLastError leaves a sticky error from
     // the caller's earlier work in place for the caller to see
     return hipPeekAtLastError();
