@@ -30,6 +30,25 @@ __device__ __forceinline__ floatx4 mfma16x16x32(bf16x8 a, bf16x8 b, floatx4 c)
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef int intx8 __attribute__((ext_vector_type(8)));
+
+// D[16x16] += A[16x128] * B[128x16], OCP fp8 E4M3 in, fp32 accumulate.
+// Lane l supplies A[l % 16][32 * (l / 16) + j] and B[32 * (l / 16) + j][l % 16]
+// as byte j (0..31) of its 8 registers; D layout as above. (Checked on
+// gfx950 against a float64 product of the decoded bytes.)
+__device__ __forceinline__ floatx4 mfma16x16x128_fp8(intx8 a, intx8 b, floatx4 c)
+{
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// D[16x16] += A[16x32] * B[32x16], OCP fp8 E4M3 in: lane l supplies
+// A[l % 16][8 * (l / 16) + j] and B[8 * (l / 16) + j][l % 16] as byte j (0..7).
+__device__ __forceinline__ floatx4 mfma16x16x32_fp8(uint2 a, uint2 b, floatx4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c,
+                                                     0, 0, 0);
+}
+
 // Vector types of a 16-bit storage type (fp16 or bf16): 8 elements are one
 // MFMA operand, 4 one transpose read or one partial store.
 template <typename E>

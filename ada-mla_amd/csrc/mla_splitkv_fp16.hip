@@ -133,6 +133,10 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
 {
     using T = F16Tile<HT>;
     constexpr bool kDirect = kMode == kModeDirect;
+    // fp8 cache, tiles of 32 or 64 heads: the first product on fp8 MFMAs
+    // (Q* split, below); tiles of 16 heads convert C to fp16 for it instead,
+    // where the split's fixed cost per piece exceeds what it saves
+    constexpr bool kF8M = kF8 && HT >= 32;
     static_assert(kMode == kModeBatch || !kPaged, "a paged cache comes with cu_seqlens");
     static_assert(!(kF8 && (kPaged || !__is_same(E, _Float16))), "fp8 cache: packed layout, fp16 query");
     using E8 = typename Vec<E>::v8;
@@ -195,7 +199,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     // that no block straddles a page (tokens before p_lo are masked). Every
     // wave walks the same pieces and, per piece, passes the same number of
     // barriers (nblk + 5; nblk + 4 for a single sequence, whose prologue
-    // loads need no piece-start barrier).
+    // loads need no piece-start barrier; one more with an fp8 cache and
+    // 32 or 64 heads, before the split of Q*).
     auto for_each_piece = [&](auto &&body) {
         for (int b = b_first; b < nseq; ++b) {
             int seq_lo = 0, seq_hi = total_tokens;
@@ -407,10 +412,142 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         first_b = 0;
         prologue_issue(0, 0, lo, hi);
     }
-    auto piece_prologue = [&](int b, int seq_lo, int p_org, int p_hi) {
+    // fp8 cache: the first product runs on fp8 MFMAs with Q* split into
+    // two fp8 operands, so that C is used as stored (no conversion of the
+    // first product's operand). Head h's Q* row is scaled by 2^e_h, a power
+    // of two that puts its largest |q| in [128, 256), and
+    //   hi = fp8(2^e q),  lo = fp8(16 (2^e q - hi)),
+    // so q = 2^-e (hi + lo / 16) to about 2^-8 relative (hi holds 4
+    // significant bits, lo the next 4; 16 (2^e q - hi) is at most 2^e q in
+    // magnitude, so lo neither overflows nor, for the head's large entries,
+    // goes subnormal). The S waves accumulate the products with hi and with
+    // lo separately, combine them as hi + lo / 16 and scale by 2^-e_h in the
+    // softmax (s_qsc[h] = scale_log2 2^-e_h).
+    // 8 fp16 values -> 8 bytes of hi and of lo (byte k <- value k), two
+    // values per instruction: the scaled conversions compute fp8(v / s)
+    // and fp8 * s (round to nearest even, checked on gfx950), so with
+    // si = 2^-e and sl = 2^-(e+4):
+    //   hi = fp8(q / si),  r = q - hi * si (fp16, exact: hi * si is q
+    //   rounded to 4 significant bits, within a factor 2 of q),
+    //   lo = fp8(r / sl) = fp8(16 (2^e q - hi)).
+    auto q_split8 = [](half8 x, float si, float sl, uint2 &hi, uint2 &lo) {
+        typedef short s16x2 __attribute__((ext_vector_type(2)));
+        unsigned hv[2], lv[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const half2v q0 = half2v{x[4 * p], x[4 * p + 1]}, q1 = half2v{x[4 * p + 2], x[4 * p + 3]};
+            // (the first conversion of each register writes its low half; the
+            // old value passed for the high half is overwritten by the second)
+            s16x2 h = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(__builtin_bit_cast(s16x2, q1), q0, si, false);
+            h = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(h, q1, si, true);
+            const int hw = __builtin_bit_cast(int, h);
+            const half2v b0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hw, si, false);
+            const half2v b1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hw, si, true);
+            s16x2 l = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(__builtin_bit_cast(s16x2, q1), q0 - b0, sl, false);
+            l = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(l, q1 - b1, sl, true);
+            hv[p] = __builtin_bit_cast(unsigned, h);
+            lv[p] = __builtin_bit_cast(unsigned, l);
+        }
+        hi = uint2{hv[0], hv[1]};
+        lo = uint2{lv[0], lv[1]};
+    };
+    // The split runs once per piece, by all 8 waves, in place in the Q*
+    // slots, after a barrier that follows Q*'s arrival (piece_prologue)
+    // and before barrier A, while the first blocks are still landing: wave w
+    // converts heads kQR*w .. +kQR-1, each by kQAct lanes of kQCpl 16-byte
+    // chunks (8 values) of its 72 (64 C_N, 8 rope). A head's row keeps its
+    // place: its C_N kilobyte then holds hi (bytes 0..511) and lo
+    // (512..1023), 16-byte chunk c at c ^ (row mod 16); its 128-byte rope
+    // part holds hi (0..63) and lo (64..127), 8-byte unit u at
+    // u ^ ((row / 2) mod 8). A wave reads all its rows' chunks before it
+    // writes any, and no other wave touches them.
+    constexpr int kQR = HT / 8;                                      // heads per wave
+    constexpr int kQLR = 64 / kQR;                                   // lanes per head
+    constexpr int kQCpl = kQLR == 8 ? 9 : (kQLR == 16 ? 6 : 3);      // chunks per lane
+    constexpr int kQAct = 72 / kQCpl;                                // active lanes per head
+    static_assert(kQAct <= kQLR && kQAct * kQCpl == 72, "Q* split mapping");
+    __shared__ float s_qsc[kF8M ? HT : 1];
+    auto q_split_lds = [&]() __attribute__((always_inline)) {  // three call sites, one per role
+        int ln = lane;  // opaque: the addresses below are formed here, not kept live
+        asm volatile("" : "+v"(ln));
+        const int h = kQR * wave + ln / kQLR;
+        const int j = ln % kQLR;
+        const int rr = h % 32;
+        E *const qrow = s_ring + (T::kPre + h / 32) * T::kSlot + rr * kDV;
+        E *const qrope = s_ring + (T::kPre + h / 32) * T::kSlot + T::kRope + rr * (kDK - kDV);
+        half8 v[kQCpl];
+        // max |q| over the lane's values: packed over the fp16 bit patterns
+        // with the sign cleared (their unsigned order is the order of |q|)
+        typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+        u16x2 mb = {0, 0};
+#pragma unroll
+        for (int i = 0; i < kQCpl; ++i) {
+            const int ch = j + kQAct * i;
+            v[i] = half8{};
+            if (j < kQAct)
+                v[i] = ch < 64 ? *(const half8 *)(qrow + 8 * (ch ^ row_swizzle(rr)))
+                               : *(const half8 *)(qrope + 8 * ((ch - 64) ^ rope_swizzle(rr)));
+            const uint4 u = __builtin_bit_cast(uint4, v[i]);
+            mb = __builtin_elementwise_max(mb, __builtin_bit_cast(u16x2, u.x & 0x7fff7fffu));
+            mb = __builtin_elementwise_max(mb, __builtin_bit_cast(u16x2, u.y & 0x7fff7fffu));
+            mb = __builtin_elementwise_max(mb, __builtin_bit_cast(u16x2, u.z & 0x7fff7fffu));
+            mb = __builtin_elementwise_max(mb, __builtin_bit_cast(u16x2, u.w & 0x7fff7fffu));
+        }
+        asm volatile("" ::: "memory");  // every read of the rows above the writes below
+        // over the head's kQLR lanes (aligned groups of 8, 16 or 32):
+        // quad swaps, then the mirrored half row and row (DPP), then the
+        // other 16-lane row (v_permlane16_swap)
+        int mi = mb[0] > mb[1] ? mb[0] : mb[1];
+        mi = max(mi, __builtin_amdgcn_update_dpp(0, mi, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+        mi = max(mi, __builtin_amdgcn_update_dpp(0, mi, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+        mi = max(mi, __builtin_amdgcn_update_dpp(0, mi, 0x141, 0xF, 0xF, false));  // row_half_mirror
+        if constexpr (kQLR >= 16)
+            mi = max(mi, __builtin_amdgcn_update_dpp(0, mi, 0x140, 0xF, 0xF, false));  // row_mirror
+        if constexpr (kQLR >= 32) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(mi, mi, false, false);
+            mi = max((int)sw[0], (int)sw[1]);
+        }
+        const float amax = (float)__builtin_bit_cast(_Float16, (unsigned short)mi);
+        // amax = m 2^x, m in [0.5, 1): 2^(8 - x) amax in [128, 256)
+        const int e = 8 - __builtin_amdgcn_frexp_expf(amax);
+        const float si = __builtin_ldexpf(1.f, -e);
+        if (j == 0)
+            s_qsc[h] = scale_log2 * si;
+        unsigned char *const q8 = reinterpret_cast<unsigned char *>(qrow);
+        unsigned char *const r8 = reinterpret_cast<unsigned char *>(qrope);
+#pragma unroll
+        for (int i = 0; i < kQCpl; ++i) {
+            const int ch = j + kQAct * i;
+            if (j < kQAct) {
+                uint2 hi, lo;
+                q_split8(v[i], si, 0.0625f * si, hi, lo);
+                if (ch < 64) {
+                    const int o = 16 * ((ch >> 1) ^ (rr & 15)) + 8 * (ch & 1);
+                    *(uint2 *)(q8 + o) = hi;
+                    *(uint2 *)(q8 + 512 + o) = lo;
+                } else {
+                    const int o = 8 * ((ch - 64) ^ ((rr >> 1) & 7));
+                    *(uint2 *)(r8 + o) = hi;
+                    *(uint2 *)(r8 + 64 + o) = lo;
+                }
+            }
+        }
+    };
+
+    auto piece_prologue = [&](int b, int seq_lo, int p_org, int p_hi) __attribute__((always_inline)) {
         if (b != first_b) {
             lds_barrier();  // piece start: buffers are reused from the previous piece
             prologue_issue(b, seq_lo, p_org, p_hi);
+        }
+        if constexpr (kF8M) {
+            // Q* went out first: wait for it alone, so that the split runs
+            // while the piece's first blocks arrive
+            if (wave < 4)
+                MLA_WAIT_VMCNT(5 * T::kPre);
+            else
+                MLA_WAIT_VMCNT(4 * T::kPre);
+            lds_barrier();  // Q* has landed
+            q_split_lds();
         }
         prologue_own_wait();
     };
@@ -454,34 +591,79 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             return kk < 16 ? *(const E8 *)(slot + r * kDV + a_off[kk & 3] + 128 * (kk >> 2))
                            : *(const E8 *)(slot + r * (kDK - kDV) + a_off[kk - 12]);
         };
-        // fp8 ring: the 8 bytes of K-step kk of row r (K = 32 kk + 8 g ..),
-        // converted only where the MFMA takes them, so that the read stays
-        // in flight
+        // fp8 ring: the 8 bytes of K-step kk of row r (K = 32 kk + 8 g ..)
         auto a8_raw = [&](const unsigned char *slot8, int r, int kk) -> uint2 {
             const int ch = 2 * (kk & 15) + (g >> 1);  // 16-byte chunk within the C_N or rope part
             return kk < 16 ? *(const uint2 *)(slot8 + r * kDV + 16 * (ch ^ row_swizzle(r)) + 8 * (g & 1))
                            : *(const uint2 *)(slot8 + kF8Rope + r * (kDK - kDV) + 16 * (ch ^ ((r >> 2) & 3)) +
                                               8 * (g & 1));
         };
+        // fp8 ring: the 32 bytes of C_N K-step kq (128 wide) of row r,
+        // K = 128 kq + 32 g .. +31: stored chunks (8 kq + 2 g, +1) ^ (r mod 16)
+        // (the swizzle permutes aligned groups of 16 chunks: two per-lane
+        // offsets, by kq & 1, and immediates)
+        auto a8_wide = [&](const unsigned char *slot8, int r, int kq) -> intx8 {
+            const int c0 = 8 * (kq & 1) + 2 * g;
+            const unsigned char *row = slot8 + r * kDV + 256 * (kq >> 1);
+            const uint4 x = *(const uint4 *)(row + 16 * (c0 ^ row_swizzle(r)));
+            const uint4 y = *(const uint4 *)(row + 16 * ((c0 + 1) ^ row_swizzle(r)));
+            return intx8{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
+        };
 
         for_each_piece([&](int b, int seq_lo, int p_org, int p_lo, int p_hi) {
             const int slot_out = split + b;
             const int nblk = (p_hi - p_org + T::kBT - 1) / T::kBT;
             piece_prologue(b, seq_lo, p_org, p_hi);
-            lds_barrier();  // A: Q* and block 0 have landed
+            lds_barrier();  // A: Q* (split, with kF8M) and block 0 have landed
             // Q* fragments (B operand of S^T = C Q*^T): lane holds head
             // kSH*hg + 16*ns + l16 of the tile, dims 32*kk + 8*g .. +7. Q*
             // rows sit in the ring in the same swizzled layout as C rows.
-            E8 qf[T::kNS][kDK / 32];
+            E8 qf[kF8M ? 1 : T::kNS][kF8M ? 1 : kDK / 32];
+            // fp8 cache: lane holds head kSH*hg + 16*ns + l16, C_N dims
+            // 128 kq + 32 g .. +31 (qh / ql) and rope dims 32 rk + 8 g .. +7
+            // (qrh / qrl); qsc = scale_log2 * 2^-e of that head
+            intx8 qh[kF8M ? T::kNS : 1][4], ql[kF8M ? T::kNS : 1][4];
+            uint2 qrh[kF8M ? T::kNS : 1][2], qrl[kF8M ? T::kNS : 1][2];
+            float qsc[T::kNS];
             {
                 // head h of the tile is row h % 32 of Q* slot kPre + h / 32
 #pragma unroll
                 for (int ns = 0; ns < T::kNS; ++ns) {
                     const int h = T::kSH * hg + 16 * ns + l16;
                     const E *qs = s_ring + (T::kPre + h / 32) * T::kSlot;
+                    if constexpr (kF8M) {
+                        // the split Q* (q_split_lds): hi / lo chunks
+                        // 8 kq + 2 g, +1 of the row's C_N kilobyte and rope
+                        // units 4 rk + g
+                        const int rr = h % 32;
+                        const unsigned char *q8 = reinterpret_cast<const unsigned char *>(qs + rr * kDV);
+                        const unsigned char *r8 =
+                            reinterpret_cast<const unsigned char *>(qs + T::kRope + rr * (kDK - kDV));
 #pragma unroll
-                    for (int kk = 0; kk < kDK / 32; ++kk)
-                        qf[ns][kk] = a_at(qs, h % 32, kk);
+                        for (int kq = 0; kq < 4; ++kq) {
+                            const int c0 = 8 * kq + 2 * g;
+                            const uint4 h0 = *(const uint4 *)(q8 + 16 * (c0 ^ (rr & 15)));
+                            const uint4 h1 = *(const uint4 *)(q8 + 16 * ((c0 + 1) ^ (rr & 15)));
+                            const uint4 l0 = *(const uint4 *)(q8 + 512 + 16 * (c0 ^ (rr & 15)));
+                            const uint4 l1 = *(const uint4 *)(q8 + 512 + 16 * ((c0 + 1) ^ (rr & 15)));
+                            qh[ns][kq] = intx8{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w,
+                                               (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+                            ql[ns][kq] = intx8{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w,
+                                               (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+                        }
+#pragma unroll
+                        for (int rk = 0; rk < 2; ++rk) {
+                            const int o = 8 * ((4 * rk + g) ^ ((rr >> 1) & 7));
+                            qrh[ns][rk] = *(const uint2 *)(r8 + o);
+                            qrl[ns][rk] = *(const uint2 *)(r8 + 64 + o);
+                        }
+                        qsc[ns] = s_qsc[h];
+                    } else {
+                        qsc[ns] = scale_log2;
+#pragma unroll
+                        for (int kk = 0; kk < kDK / 32; ++kk)
+                            qf[ns][kk] = a_at(qs, h % 32, kk);
+                    }
                 }
             }
             lds_barrier();  // B: the Q* slots are free again
@@ -506,6 +688,44 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
 #pragma unroll
                         for (int j = 0; j < T::kChains; ++j)
                             acc[ns][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (kF8M) {
+                        // 4 C_N K-steps of 128 (operand reads one step
+                        // ahead of their MFMAs) and 2 rope K-steps of 32;
+                        // chain 2j (+ 1): products with hi (lo)
+                        const unsigned char *cslot8 = ring8 + (blk % T::kRing) * (T::kSlot * 2);
+                        const int rr = 16 * th + l16;
+                        auto hc = [](int k) { return T::kChains == 2 ? 0 : 2 * (k & 1); };
+                        intx8 aw[2];
+                        uint2 ar[2];
+                        aw[0] = a8_wide(cslot8, rr, 0);
+#pragma unroll
+                        for (int kq = 0; kq < 4; ++kq) {
+                            if (kq + 1 < 4)
+                                aw[(kq + 1) & 1] = a8_wide(cslot8, rr, kq + 1);
+                            if (kq == 3) {
+                                ar[0] = a8_raw(cslot8, rr, 16);
+                                ar[1] = a8_raw(cslot8, rr, 17);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                            for (int ns = 0; ns < T::kNS; ++ns) {
+                                acc[ns][hc(kq)] = mfma16x16x128_fp8(aw[kq & 1], qh[ns][kq], acc[ns][hc(kq)]);
+                                acc[ns][hc(kq) + 1] = mfma16x16x128_fp8(aw[kq & 1], ql[ns][kq], acc[ns][hc(kq) + 1]);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+#pragma unroll
+                        for (int rk = 0; rk < 2; ++rk) {
+#pragma unroll
+                            for (int ns = 0; ns < T::kNS; ++ns) {
+                                acc[ns][hc(rk)] = mfma16x16x32_fp8(ar[rk], qrh[ns][rk], acc[ns][hc(rk)]);
+                                acc[ns][hc(rk) + 1] = mfma16x16x32_fp8(ar[rk], qrl[ns][rk], acc[ns][hc(rk) + 1]);
+                            }
+                        }
+                    } else {
+                    // 18 K-steps of 32; the operand reads go out in batches
+                    // of 3 K-steps, two batches ahead of the MFMAs that
+                    // consume them
                     constexpr int kB = 3;                 // K-steps per batch
                     constexpr int kNB = kDK / 32 / kB;    // batches (6)
                     using AB = typename std::conditional<kF8, uint2, E8>::type;
@@ -522,11 +742,12 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     };
                     load_batch(0, 0);
                     load_batch(1, kB);
-                    // fp8: each K-step's operand is converted one K-step
-                    // ahead, into the other of two register sets, so that
-                    // the conversions run while the previous MFMAs do (one
-                    // set made every conversion wait for the MFMAs before it
-                    // to read their operand, and every MFMA for its operand)
+                    // fp8 (16-head tiles): each K-step's operand is
+                    // converted to fp16 one K-step ahead, into the other of
+                    // two register sets, so that the conversions run while
+                    // the previous MFMAs do (one set made every conversion
+                    // wait for the MFMAs before it to read their operand,
+                    // and every MFMA for its operand)
                     E8 cv[2];
                     if constexpr (kF8)
                         cv[0] = f8_to_f16(ab[0][0]);
@@ -554,20 +775,32 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         }
                         __builtin_amdgcn_sched_barrier(0);
                     }
+                    }
                     // ---- online softmax of this wave's 16 tokens, per head
 #pragma unroll
                     for (int ns = 0; ns < T::kNS; ++ns) {
-                        floatx4 st = acc[ns][0];
+                        floatx4 st;
+                        if constexpr (kF8M) {
+                            floatx4 sh = acc[ns][0], sl = acc[ns][1];
 #pragma unroll
-                        for (int j = 1; j < T::kChains; ++j)
-                            st += acc[ns][j];
+                            for (int j = 2; j < T::kChains; j += 2) {
+                                sh += acc[ns][j];
+                                sl += acc[ns][j + 1];
+                            }
+                            st = sh + sl * 0.0625f;
+                        } else {
+                            st = acc[ns][0];
+#pragma unroll
+                            for (int j = 1; j < T::kChains; ++j)
+                                st += acc[ns][j];
+                        }
                         float sv[4];
                         float mx = -INFINITY;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int tok = t0 + 4 * g + i;
                             const bool valid = kPaged ? (tok >= p_lo && tok < p_hi) : tok < p_hi;
-                            sv[i] = valid ? st[i] * scale_log2 : -INFINITY;
+                            sv[i] = valid ? st[i] * qsc[ns] : -INFINITY;
                             mx = fmaxf(mx, sv[i]);
                         }
                         mx = max_over_lane_groups(mx);
@@ -611,13 +844,17 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 lds_barrier();
             }
             // ---- epilogue: this half's running max and sum per head; the
-            // first half merges both and writes the piece's m and l
+            // first half merges both and writes the piece's m and l (the
+            // LDS addresses formed here from an opaque copy of the lane, not
+            // kept live, or spilled, through the piece)
+            int el16 = l16;
+            asm volatile("" : "+v"(el16));
 #pragma unroll
             for (int ns = 0; ns < T::kNS; ++ns) {
                 const float ls = sum_over_lane_groups(l_lane[ns]);
                 if (g == 0) {
-                    s_m[0][m_at(T::kSH * hg + 16 * ns + l16, th)] = m_run[ns];
-                    s_l[th][T::kSH * hg + 16 * ns + l16] = ls;
+                    s_m[0][m_at(T::kSH * hg + 16 * ns + el16, th)] = m_run[ns];
+                    s_l[th][T::kSH * hg + 16 * ns + el16] = ls;
                 }
             }
             lds_barrier();

@@ -6,7 +6,9 @@ no reference fp8 path (README.md:408 lists it as future work).
 
 Tolerance as for fp16: atol = rtol = 1e-2 and mean relative error < 5e-3 --
 the dequantisation itself is exact (every E4M3 value is an fp16 value), so
-only the kernel's own rounding (fp16 P, fp16 partials and output) remains.
+only the kernel's own rounding remains: fp16 P, fp16 partials and output,
+and, with 32- or 64-head tiles, Q* held as two fp8 parts (about 8
+significant bits, each head scaled by a power of two) for the first product.
 """
 import numpy as np
 import pytest
@@ -26,9 +28,11 @@ def _fp8_inputs(n_h, n, seed, scale):
     return q, c8, c_deq
 
 
-def _check(got, ref, what):
+def _check(got, ref, what, scale=1.0):
+    # scale: the cache's dequantisation scale when the data are not of
+    # order one (the absolute tolerance is for unit-scale values)
     assert np.isfinite(got).all(), what
-    np.testing.assert_allclose(got, ref, atol=1e-2, rtol=1e-2, err_msg=what)
+    np.testing.assert_allclose(got, ref, atol=1e-2 * scale, rtol=1e-2, err_msg=what)
     rel = np.abs(got - ref).mean() / max(np.abs(ref).mean(), 1e-30)
     assert rel < 5e-3, f"{what}: mean relative error {rel:.3e}"
 
@@ -65,6 +69,33 @@ def test_fp8_split_invariance_and_single_token():
     # one token: the output is that token's dequantised C_N row, rounded to fp16
     want = np.repeat(cd1[:, :512], 16, axis=0).astype(np.float16).astype(np.float64)
     assert np.array_equal(out.double().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("n_h", [32, 128])
+@pytest.mark.parametrize("q_scale,c_scale", [(2.0 ** 4, 2.0 ** -4), (2.0 ** -8, 2.0 ** 8)])
+def test_fp8_query_dynamic_range(n_h, q_scale, c_scale):
+    # With 32- or 64-head tiles the first product runs on fp8 MFMAs, with
+    # each head's Q* row scaled by a power of two and split into two fp8
+    # operands. Rows of different magnitudes (per-head factors 2^-2 .. 2^2,
+    # times q_scale, offset by the cache scale so that the logits stay of
+    # order one), entries far outside fp8's range either way, and an
+    # all-zero row (uniform weights) must all come out right. N = 65536 at
+    # 128 heads is a 64-head-tile plan.
+    n = 65536 if n_h == 128 else 20000
+    print(f"fp8 dynamic range n_h={n_h} q_scale={q_scale}", flush=True)
+    q = synthetic.normal((n_h, 576), 77, np.float32)
+    q = q * (2.0 ** np.linspace(-2.0, 2.0, n_h))[:, None] * q_scale
+    q[3] = 0.0
+    q16 = q.astype(np.float16)
+    c8 = torch.from_numpy(synthetic.normal((n, 576), 78, np.float32)).to(torch.float8_e4m3fn)
+    cd = c8.float().double().numpy() * c_scale
+    out = capi.decode_split_fp8(torch.from_numpy(q16).cuda(), c8.cuda(), c_scale)
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    ref = O.closed_form(q16, cd)
+    _check(got, ref, f"n_h={n_h} q_scale={q_scale}", scale=max(1.0, c_scale))
+    # the zero row: every token weighs the same
+    np.testing.assert_allclose(got[3], cd[:, :512].mean(axis=0), atol=1e-3 * c_scale, rtol=1e-2)
 
 
 def test_fp8_batched_with_empty():
