@@ -33,6 +33,7 @@ _SIGNATURES = {
     "mla_status_string": (ctypes.c_char_p, [_i]),
     "mla_last_hip_error": (_i, []),
     "mla_decode_split_num_splits": (_i, [_i, _i, _i, _u]),
+    "mla_decode_split_head_tile": (_i, [_i, _i, _i, _u]),
     "mla_decode_split_launches": (_i, [_i, _i, _i, _u]),
     "mla_decode_split_workspace_size": (_sz, [_i, _i, _i]),
     "mla_decode_split_fp16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),

@@ -132,7 +132,7 @@ namespace {
 Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
                   int num_splits, int cu_count, CacheKind cache, bool f32_partials)
 {
-    const bool paged = cache != CacheKind::kPacked;  // pieces start page-aligned: one more block
+    const bool paged = cache == CacheKind::kPaged;  // pieces start page-aligned: one more block
     Plan p{};
     if (total_tokens <= 0) {
         p.head_tile = fp32 ? 16 : (num_heads % 64 == 0) ? 64 : (num_heads % 32 == 0) ? 32 : 16;
@@ -411,6 +411,15 @@ int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits, u
     return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
                           (flags & MLA_FLAG_FP32_PARTIALS) != 0)
         .n_chunks;
+}
+
+int mla_decode_split_head_tile(int num_heads, int seq_length, int num_splits, unsigned flags)
+{
+    if (!mla::heads_ok(num_heads) || seq_length < 1)
+        return 0;
+    return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
+                          (flags & MLA_FLAG_FP32_PARTIALS) != 0)
+        .head_tile;
 }
 
 int mla_decode_split_launches(int num_heads, int seq_length, int num_splits, unsigned flags)

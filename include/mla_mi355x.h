@@ -84,6 +84,15 @@ int mla_last_hip_error(void);
 int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits,
                                 unsigned flags);
 
+/* Heads per workgroup (16, 32 or 64) of the plan that
+ * mla_decode_split_fp16_ex uses for these arguments and flags on the current
+ * device, and mla_decode_split_fp8 for the same sizes; 0 for invalid sizes.
+ * With an fp8 cache, tiles of 32 or 64 heads run the first product on fp8
+ * MFMAs (Q* split in two fp8 parts), tiles of 16 convert C to fp16. No
+ * counterpart in the reference. */
+int mla_decode_split_head_tile(int num_heads, int seq_length, int num_splits,
+                               unsigned flags);
+
 /* Kernel launches (1 or 2, see MLA_FLAG_TWO_LAUNCHES) that
  * mla_decode_split_fp16_ex makes for these arguments and flags on the
  * current device; 0 for invalid sizes. No counterpart in the reference, whose

@@ -258,6 +258,19 @@ def test_single_launch_choice():
     assert f(24, 100, 0, 0) == 0 and f(128, 0, 0, 0) == 0
 
 
+def test_head_tile_query():
+    # the plan's heads per workgroup: 64 at long N, 16 at N = 4096 (eight
+    # tiles fill the CUs), 32 when a requested split count leaves room; 0 for
+    # invalid sizes
+    lib = capi.load()
+    f = lib.mla_decode_split_head_tile
+    assert f(128, 65536, 0, 0) == 64
+    assert f(128, 4096, 0, 0) == 16
+    assert f(32, 20000, 200, 0) == 32
+    assert f(16, 32768, 0, 0) == 16
+    assert f(24, 100, 0, 0) == 0 and f(128, 0, 0, 0) == 0
+
+
 def test_block_projection_argument_errors():
     lib = capi.load()
     for fn in ("mla_absorb_query_fp16", "mla_absorb_query_bf16"):

@@ -79,9 +79,11 @@ def test_fp8_query_dynamic_range(n_h, q_scale, c_scale):
     # operands. Rows of different magnitudes (per-head factors 2^-2 .. 2^2,
     # times q_scale, offset by the cache scale so that the logits stay of
     # order one), entries far outside fp8's range either way, and an
-    # all-zero row (uniform weights) must all come out right. N = 65536 at
-    # 128 heads is a 64-head-tile plan.
-    n = 65536 if n_h == 128 else 20000
+    # all-zero row (uniform weights) must all come out right. The plans are
+    # a 64-head tile (128 heads, N = 65536) and a 32-head tile (32 heads,
+    # 200 splits of N = 20000).
+    n, splits = (65536, 0) if n_h == 128 else (20000, 200)
+    assert capi.load().mla_decode_split_head_tile(n_h, n, splits, 0) == (64 if n_h == 128 else 32)
     print(f"fp8 dynamic range n_h={n_h} q_scale={q_scale}", flush=True)
     q = synthetic.normal((n_h, 576), 77, np.float32)
     q = q * (2.0 ** np.linspace(-2.0, 2.0, n_h))[:, None] * q_scale
@@ -89,7 +91,7 @@ def test_fp8_query_dynamic_range(n_h, q_scale, c_scale):
     q16 = q.astype(np.float16)
     c8 = torch.from_numpy(synthetic.normal((n, 576), 78, np.float32)).to(torch.float8_e4m3fn)
     cd = c8.float().double().numpy() * c_scale
-    out = capi.decode_split_fp8(torch.from_numpy(q16).cuda(), c8.cuda(), c_scale)
+    out = capi.decode_split_fp8(torch.from_numpy(q16).cuda(), c8.cuda(), c_scale, num_splits=splits)
     torch.cuda.synchronize()
     got = out.double().cpu().numpy()
     ref = O.closed_form(q16, cd)
