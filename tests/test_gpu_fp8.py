@@ -118,6 +118,23 @@ def test_fp8_batched_with_empty():
             _check(got[b], ref[b], f"seq {b}")
 
 
+def test_fp8_config5_batched():
+    # BASELINE config 5's shape with an fp8 cache: 64-head tiles whose chunks
+    # hold pieces of up to three sequences, each piece splitting its own Q*
+    # into fp8 parts after the piece-start barrier
+    print("fp8 config 5", flush=True)
+    seqlens = synthetic.batched_seqlens(32, seed=42)
+    q, _, cu = synthetic.batched_inputs(128, seqlens, seed=42)
+    c8 = torch.from_numpy(synthetic.normal((int(cu[-1]), 576), 43, np.float32)).to(torch.float8_e4m3fn)
+    cd = c8.float().double().numpy()
+    out = capi.decode_split_batched_fp8(torch.from_numpy(q).cuda(), c8.cuda(), 1.0, torch.from_numpy(cu).cuda())
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    for b in range(32):
+        lo, hi = cu[b], cu[b + 1]
+        _check(got[b], O.closed_form(q[b], cd[lo:hi]), f"config 5 seq {b} N={hi - lo}")
+
+
 def test_fp8_batched_many_items_with_empty():
     # 24 sequences x 128 heads: the combine merges several tiles per wave
     seqlens = np.random.default_rng(6).integers(2, 600, size=24)
