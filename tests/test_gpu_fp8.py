@@ -72,7 +72,7 @@ def test_fp8_split_invariance_and_single_token():
 
 
 @pytest.mark.parametrize("n_h", [32, 128])
-@pytest.mark.parametrize("q_scale,c_scale", [(2.0 ** 4, 2.0 ** -4), (2.0 ** -8, 2.0 ** 8)])
+@pytest.mark.parametrize("q_scale,c_scale", [(2.0 ** 4, 2.0 ** -4), (2.0 ** -8, 2.0 ** 8), (2.0 ** 10, 2.0 ** -6)])
 def test_fp8_query_dynamic_range(n_h, q_scale, c_scale):
     # With 32- or 64-head tiles the first product runs on fp8 MFMAs, with
     # each head's Q* row scaled by a power of two and split into two fp8
