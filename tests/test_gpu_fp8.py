@@ -118,6 +118,18 @@ def test_fp8_batched_with_empty():
             _check(got[b], ref[b], f"seq {b}")
 
 
+@pytest.mark.parametrize("n_h,n,tile", [(96, 20000, 32), (192, 40000, 64), (64, 30000, 32)])
+def test_fp8_several_head_tiles(n_h, n, tile):
+    # fp8 first product on three head tiles of 32 or 64 heads per chunk
+    # (the Q* split of each tile in its own workgroups)
+    assert capi.load().mla_decode_split_head_tile(n_h, n, 0, 0) == tile
+    print(f"fp8 n_h={n_h} N={n} head tile {tile}", flush=True)
+    q, c8, cd = _fp8_inputs(n_h, n, seed=90 + n_h, scale=0.5)
+    out = capi.decode_split_fp8(torch.from_numpy(q).cuda(), c8.cuda(), 0.5)
+    torch.cuda.synchronize()
+    _check(out.double().cpu().numpy(), O.closed_form(q, cd), f"n_h={n_h} N={n}")
+
+
 def test_fp8_config5_batched():
     # BASELINE config 5's shape with an fp8 cache: 64-head tiles whose chunks
     # hold pieces of up to three sequences, each piece splitting its own Q*
