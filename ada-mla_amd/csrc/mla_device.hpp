@@ -136,9 +136,16 @@ __device__ __forceinline__ void store_nt(float *p, float v)
 {
     asm volatile("global_store_dword %0, %1, off nt" ::"v"(p), "v"(v));
 }
+// A store of more than 64 bits of data reads its data VGPRs after issue: on
+// gfx950 a VALU write to those registers needs two wait states after the
+// store. The compiler inserts them for stores it generates but cannot see
+// into inline asm, so the asm carries them itself (s_nop 1). Without them a
+// VALU that reused the registers right after the store corrupted the first
+// two dwords of some lanes' 16 bytes (measured: fp32 partials of a few
+// lanes per slot, depending on the schedule).
 __device__ __forceinline__ void store_nt(floatx4 *p, floatx4 v)
 {
-    asm volatile("global_store_dwordx4 %0, %1, off nt" ::"v"(p), "v"(v));
+    asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" ::"v"(p), "v"(v));
 }
 template <typename V4>  // 4 x 16-bit elements
 __device__ __forceinline__ void store_nt8(V4 *p, V4 v)
