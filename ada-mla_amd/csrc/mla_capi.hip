@@ -129,7 +129,7 @@ double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, in
 
 namespace {
 
-Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
+Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch, bool seqlens,
                   int num_splits, int cu_count, CacheKind cache, bool f32_partials)
 {
     const bool paged = cache == CacheKind::kPaged;  // pieces start page-aligned: one more block
@@ -184,7 +184,7 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
         for (int w = w_lo; w <= w_hi; ++w) {
             set_chunks(c, total_tokens, batch, w);
             const double us = modelled_us(c, num_heads, total_tokens, batch, cu_count, paged,
-                                          batch == 1 && cache != CacheKind::kPaged);
+                                          !seqlens && cache != CacheKind::kPaged);
             if (best_us == 0.0 || us < best_us) {
                 best = c;
                 best_us = us;
@@ -199,27 +199,27 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch,
 // compute_plan searches a few hundred candidate plans (a few us of host
 // time); decode loops repeat the same arguments, so each host thread keeps
 // its last few plans.
-Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
+Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch, bool seqlens,
                int num_splits, int cu_count, CacheKind kind, bool f32_partials)
 {
     struct Entry {
-        int key[8];
+        int key[9];
         Plan plan;
     };
     constexpr int kEntries = 16;
     thread_local Entry cache[kEntries];
     thread_local int filled = 0, next = 0;
-    const int key[8] = {fp32, num_heads, total_tokens, batch, num_splits, cu_count, (int)kind, f32_partials};
+    const int key[9] = {fp32, num_heads, total_tokens, batch, seqlens, num_splits, cu_count, (int)kind, f32_partials};
     for (int e = 0; e < filled; ++e) {
         bool hit = true;
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < 9; ++k)
             hit = hit && cache[e].key[k] == key[k];
         if (hit)
             return cache[e].plan;
     }
-    const Plan p = compute_plan(fp32, num_heads, total_tokens, batch, num_splits, cu_count, kind, f32_partials);
+    const Plan p = compute_plan(fp32, num_heads, total_tokens, batch, seqlens, num_splits, cu_count, kind, f32_partials);
     Entry &slot = cache[next];
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < 9; ++k)
         slot.key[k] = key[k];
     slot.plan = p;
     next = (next + 1) % kEntries;
@@ -251,11 +251,11 @@ namespace {
 
 // Workspace of the 16-bit paths: enough for either partial precision (the
 // plans of the two may differ).
-size_t split_workspace_bytes(int num_heads, int total_tokens, int batch, int num_splits)
+size_t split_workspace_bytes(int num_heads, int total_tokens, int batch, bool seqlens, int num_splits)
 {
     const int cu = current_cu_count();
-    const Plan a = make_plan(false, num_heads, total_tokens, batch, num_splits, cu, CacheKind::kPacked, false);
-    const Plan b = make_plan(false, num_heads, total_tokens, batch, num_splits, cu, CacheKind::kPacked, true);
+    const Plan a = make_plan(false, num_heads, total_tokens, batch, seqlens, num_splits, cu, CacheKind::kPacked, false);
+    const Plan b = make_plan(false, num_heads, total_tokens, batch, seqlens, num_splits, cu, CacheKind::kPacked, true);
     return std::max(partials_bytes(a, num_heads), partials_bytes(b, num_heads));
 }
 
@@ -308,12 +308,12 @@ int run_decode(Dtype dt, const void *query, const void *cache, const int *cu_seq
     const CacheKind kind = paging != nullptr ? CacheKind::kPaged
                            : dt == Dtype::kF8Cache ? CacheKind::kF8 : CacheKind::kPacked;
     const int cu = current_cu_count();
-    Plan p = make_plan(fp32, num_heads, total_tokens, batch, num_splits, cu, kind, f32_part);
+    Plan p = make_plan(fp32, num_heads, total_tokens, batch, cu_seqlens != nullptr, num_splits, cu, kind, f32_part);
     if (workspace_bytes < partials_bytes(p, num_heads))
         return MLA_STATUS_WORKSPACE_TOO_SMALL;
     const bool tr_load = (flags & MLA_FLAG_SCALAR_TRANSPOSE) == 0;
     if (split && combine)
-        p.merge = choose_merge(p, batch == 1 && !fp32 && !paging, flags);
+        p.merge = choose_merge(p, batch == 1 && !cu_seqlens && !fp32 && !paging, flags);
     p.part_plain = choose_part_plain(p, batch, num_heads, cu);
 
     Problem pb;
@@ -408,7 +408,7 @@ int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits, u
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
+    return mla::make_plan(false, num_heads, seq_length, 1, false, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
                           (flags & MLA_FLAG_FP32_PARTIALS) != 0)
         .n_chunks;
 }
@@ -417,7 +417,7 @@ int mla_decode_split_head_tile(int num_heads, int seq_length, int num_splits, un
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    return mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
+    return mla::make_plan(false, num_heads, seq_length, 1, false, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
                           (flags & MLA_FLAG_FP32_PARTIALS) != 0)
         .head_tile;
 }
@@ -426,7 +426,7 @@ int mla_decode_split_launches(int num_heads, int seq_length, int num_splits, uns
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    const mla::Plan p = mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(),
+    const mla::Plan p = mla::make_plan(false, num_heads, seq_length, 1, false, num_splits, mla::current_cu_count(),
                                        mla::CacheKind::kPacked, (flags & MLA_FLAG_FP32_PARTIALS) != 0);
     return mla::choose_merge(p, true, flags) == mla::kMergeCombine ? 2 : 1;
 }
@@ -435,7 +435,7 @@ size_t mla_decode_split_workspace_size(int num_heads, int seq_length, int num_sp
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    return mla::split_workspace_bytes(num_heads, seq_length, 1, num_splits);
+    return mla::split_workspace_bytes(num_heads, seq_length, 1, false, num_splits);
 }
 
 int mla_decode_split_fp16_ex(const void *query, const void *cache, void *out,
@@ -463,7 +463,7 @@ int mla_decode_split_fp16_noalloc(const void *query, const void *cache, void *ou
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return MLA_STATUS_INVALID_VALUE;
     // the same plan as mla_decode_split_fp16; its partials must fit the scratch
-    const mla::Plan p = mla::make_plan(false, num_heads, seq_length, 1, num_splits, mla::current_cu_count(),
+    const mla::Plan p = mla::make_plan(false, num_heads, seq_length, 1, false, num_splits, mla::current_cu_count(),
                                        mla::CacheKind::kPacked, false);
     if (mla::partials_bytes(p, num_heads) > (size_t)MLA_NOALLOC_SCRATCH_BYTES)
         return MLA_STATUS_SCRATCH_EXCEEDED;
@@ -499,7 +499,7 @@ size_t mla_decode_fused_workspace_size(int num_heads, int seq_length, int num_sp
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    const mla::Plan p = mla::make_plan(true, num_heads, seq_length, 1, num_splits, mla::current_cu_count());
+    const mla::Plan p = mla::make_plan(true, num_heads, seq_length, 1, false, num_splits, mla::current_cu_count());
     return mla::partials_bytes(p, num_heads);
 }
 
@@ -519,7 +519,7 @@ size_t mla_decode_split_batched_workspace_size(int batch, int num_heads, int tot
 {
     if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
         return 0;
-    return mla::split_workspace_bytes(num_heads, total_tokens, batch, num_splits);
+    return mla::split_workspace_bytes(num_heads, total_tokens, batch, true, num_splits);
 }
 
 int mla_decode_split_batched_fp16(const void *query, const void *cache, const int *cu_seqlens,
@@ -539,7 +539,7 @@ size_t mla_decode_paged_workspace_size(int batch, int num_heads, int total_token
 {
     if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
         return 0;
-    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, num_splits,
+    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, true, num_splits,
                                        mla::current_cu_count(), mla::CacheKind::kPaged);
     return mla::partials_bytes(p, num_heads);
 }
@@ -589,7 +589,7 @@ size_t mla_decode_split_fp8_workspace_size(int batch, int num_heads, int total_t
 {
     if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
         return 0;
-    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, num_splits,
+    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, true, num_splits,
                                        mla::current_cu_count(), mla::CacheKind::kF8);
     return mla::partials_bytes(p, num_heads);
 }

@@ -94,7 +94,9 @@ int current_cu_count();
 // returns MLA_STATUS_HIP_ERROR.
 int record_hip_error(hipError_t e);
 
-Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch,
+// seqlens: the call passes cu_seqlens (a batch, possibly of one sequence);
+// only a single sequence without cu_seqlens can take the one-launch plan.
+Plan make_plan(bool fp32, int num_heads, int total_tokens, int batch, bool seqlens,
                int num_splits, int cu_count, CacheKind cache = CacheKind::kPacked,
                bool f32_partials = false);
 size_t partials_bytes(const Plan &p, int num_heads);

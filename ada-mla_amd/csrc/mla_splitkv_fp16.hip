@@ -430,21 +430,33 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     //   hi = fp8(q / si),  r = q - hi * si (fp16, exact: hi * si is q
     //   rounded to 4 significant bits, within a factor 2 of q),
     //   lo = fp8(r / sl) = fp8(16 (2^e q - hi)).
-    auto q_split8 = [](half8 x, float si, float sl, uint2 &hi, uint2 &lo) {
+    // kHalf: for heads whose largest |q| is 2^15 or more. Rounded to 4
+    // significant bits, an entry of 63488 or more becomes 65536, which fp16
+    // cannot hold (hi * si would be inf), so such heads form the residual at
+    // half scale: r / 2 = q / 2 - hi * (si / 2), both terms exact in fp16
+    // (q / 2 loses nothing for |q| >= 2^-14, and smaller entries are below
+    // 2^-29 of the head's maximum), and lo = fp8((r / 2) / (sl / 2)).
+    auto q_split8 = [](half8 x, float si, float sl, uint2 &hi, uint2 &lo, auto kHalf) {
         typedef short s16x2 __attribute__((ext_vector_type(2)));
+        constexpr bool kH = decltype(kHalf)::value;
+        const float sb = kH ? 0.5f * si : si, slb = kH ? 0.5f * sl : sl;
         unsigned hv[2], lv[2];
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-            const half2v q0 = half2v{x[4 * p], x[4 * p + 1]}, q1 = half2v{x[4 * p + 2], x[4 * p + 3]};
+            half2v q0 = half2v{x[4 * p], x[4 * p + 1]}, q1 = half2v{x[4 * p + 2], x[4 * p + 3]};
             // (the first conversion of each register writes its low half; the
             // old value passed for the high half is overwritten by the second)
             s16x2 h = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(__builtin_bit_cast(s16x2, q1), q0, si, false);
             h = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(h, q1, si, true);
             const int hw = __builtin_bit_cast(int, h);
-            const half2v b0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hw, si, false);
-            const half2v b1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hw, si, true);
-            s16x2 l = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(__builtin_bit_cast(s16x2, q1), q0 - b0, sl, false);
-            l = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(l, q1 - b1, sl, true);
+            const half2v b0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hw, sb, false);
+            const half2v b1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hw, sb, true);
+            if constexpr (kH) {
+                q0 *= (_Float16)0.5f;
+                q1 *= (_Float16)0.5f;
+            }
+            s16x2 l = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(__builtin_bit_cast(s16x2, q1), q0 - b0, slb, false);
+            l = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(l, q1 - b1, slb, true);
             hv[p] = __builtin_bit_cast(unsigned, h);
             lv[p] = __builtin_bit_cast(unsigned, l);
         }
@@ -511,6 +523,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         // amax = m 2^x, m in [0.5, 1): 2^(8 - x) amax in [128, 256)
         const int e = 8 - __builtin_amdgcn_frexp_expf(amax);
         const float si = __builtin_ldexpf(1.f, -e);
+        const bool big = amax >= 32768.f;  // the half-scale residual (q_split8)
         if (j == 0)
             s_qsc[h] = scale_log2 * si;
         unsigned char *const q8 = reinterpret_cast<unsigned char *>(qrow);
@@ -520,7 +533,10 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             const int ch = j + kQAct * i;
             if (j < kQAct) {
                 uint2 hi, lo;
-                q_split8(v[i], si, 0.0625f * si, hi, lo);
+                if (big)
+                    q_split8(v[i], si, 0.0625f * si, hi, lo, std::true_type{});
+                else
+                    q_split8(v[i], si, 0.0625f * si, hi, lo, std::false_type{});
                 if (ch < 64) {
                     const int o = 16 * ((ch >> 1) ^ (rr & 15)) + 8 * (ch & 1);
                     *(uint2 *)(q8 + o) = hi;

@@ -39,7 +39,7 @@ extern "C" {
 
 #define MLA_HEAD_DIM_K 576 /* mla.py:33 HEAD_DIM_K = HEAD_DIM_C + HEAD_DIM_ROPE */
 #define MLA_HEAD_DIM_V 512 /* mla.py:31 HEAD_DIM_C */
-#define MLA_ABI_VERSION 1
+#define MLA_ABI_VERSION 2 /* 2: mla_project_output_workspace_size takes d_model; status 5 added */
 
 #define MLA_STATUS_SUCCESS 0
 #define MLA_STATUS_INVALID_VALUE 1       /* null pointer or unsupported size */

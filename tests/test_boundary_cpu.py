@@ -28,7 +28,7 @@ def test_library_exports_every_declared_function():
 
 def test_abi_version_and_status_strings():
     lib = capi.load()
-    assert lib.mla_abi_version() == 1
+    assert lib.mla_abi_version() == 2
     assert lib.mla_status_string(0) == b"success"
     assert b"workspace" in lib.mla_status_string(3)
     assert lib.mla_status_string(99) == b"unknown status"
@@ -67,7 +67,7 @@ def test_split_count_is_clamped_to_blocks():
     assert lib.mla_decode_split_workspace_size(128, 40, 1000) == lib.mla_decode_split_workspace_size(128, 40, 2)
 
 
-FAKE = 0x10000  # never dereferenced: every call below returns before any launch
+FAKE = 0x10000  # never dereferenced: every call below returns before any launch, or (without a GPU) fails at it
 
 
 @pytest.mark.parametrize("args,code", [
@@ -324,3 +324,23 @@ def test_fp8_argument_errors():
     assert g(FAKE, FAKE, 1.0, None, FAKE, FAKE, 1 << 30, 4, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
     assert lib.mla_decode_split_fp8_workspace_size(0, 128, 10, 0) == 0
     assert lib.mla_decode_split_fp8_workspace_size(1, 128, 10, 0) > 0
+
+
+@pytest.mark.parametrize("fn", ["mla_decode_split_batched_fp16", "mla_decode_split_batched_bf16",
+                                "mla_decode_split_batched_fp8"])
+@pytest.mark.parametrize("splits", [0, 1])
+def test_batched_single_sequence_reaches_the_launch(fn, splits):
+    # A batch of one sequence with a one-split plan once took the one-launch
+    # path, which rejects cu_seqlens before launching (hipErrorInvalidValue).
+    # Here, with no GPU, the call must get as far as the launch itself, which
+    # then fails for want of a device. With a GPU present the launch would run
+    # on the never-dereferenced FAKE pointers, so the test only runs without
+    # one (the GPU parity of this case is test_gpu_parity.py's
+    # test_batched_single_sequence).
+    if torch.cuda.device_count() > 0:
+        pytest.skip("launch-reaching CPU check: needs a machine without a GPU")
+    lib = capi.load()
+    f = getattr(lib, fn)
+    args = (FAKE, FAKE) + ((1.0,) if fn.endswith("fp8") else ()) + (FAKE, FAKE, FAKE, 1 << 30, 1, 128, 100, splits, None)
+    assert f(*args) == capi.STATUS_HIP_ERROR
+    assert lib.mla_last_hip_error() != 1  # not hipErrorInvalidValue from the plan/launch mismatch

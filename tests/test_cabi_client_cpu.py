@@ -23,7 +23,7 @@ def client():
 def test_abi_mode_without_gpu(client):
     r = subprocess.run([client, "--abi"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stderr
-    assert "abi_version 1" in r.stdout
+    assert "abi_version 2" in r.stdout
     assert "status 3: workspace too small" in r.stdout
 
 

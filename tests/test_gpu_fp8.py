@@ -100,6 +100,31 @@ def test_fp8_query_dynamic_range(n_h, q_scale, c_scale):
     np.testing.assert_allclose(got[3], cd[:, :512].mean(axis=0), atol=1e-3 * c_scale, rtol=1e-2)
 
 
+@pytest.mark.parametrize("n_h", [128, 32])
+def test_fp8_query_near_fp16_max(n_h):
+    # Heads whose largest |q| lies in [2^15, 65504]: rounded to the split's 4
+    # significant bits such an entry can become 65536, beyond fp16, so these
+    # heads form the second fp8 part at half scale. Rows scaled to maxima of
+    # 65504, 64000, 63488, 40000 and 32768 (and, for contrast, 30000), with a
+    # cache scale that keeps the logits of order one.
+    n, splits = (65536, 0) if n_h == 128 else (20000, 200)
+    assert capi.load().mla_decode_split_head_tile(n_h, n, splits, 0) == (64 if n_h == 128 else 32)
+    print(f"fp8 query near fp16 max n_h={n_h}", flush=True)
+    q = synthetic.normal((n_h, 576), 91, np.float32)
+    tops = np.array([65504.0, 64000.0, 63488.0, 40000.0, 32768.0, 30000.0])
+    amax = tops[np.arange(n_h) % len(tops)]
+    q = q / np.abs(q).max(axis=1, keepdims=True) * amax[:, None]
+    q16 = q.astype(np.float16)
+    assert np.isfinite(q16).all() and np.abs(q16).max() == 65504.0
+    c_scale = 2.0 ** -13
+    c8 = torch.from_numpy(synthetic.normal((n, 576), 92, np.float32)).to(torch.float8_e4m3fn)
+    cd = c8.float().double().numpy() * c_scale
+    out = capi.decode_split_fp8(torch.from_numpy(q16).cuda(), c8.cuda(), c_scale, num_splits=splits)
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    _check(got, O.closed_form(q16, cd), f"n_h={n_h} near fp16 max", scale=c_scale)
+
+
 def test_fp8_batched_with_empty():
     seqlens = np.array([5, 0, 17, 1, 300, 64, 0, 1000, 33])
     q, _, cu = synthetic.batched_inputs(128, seqlens, seed=9)

@@ -234,6 +234,29 @@ def test_batched_ragged_with_empty(splits):
             _check16(got[b], ref[b], f"seq {b}")
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp8"])
+@pytest.mark.parametrize("n,splits", [(100, 0), (100, 1), (3000, 1), (3000, 0)])
+def test_batched_single_sequence(dtype, n, splits):
+    # a batch of one sequence: one-split plans once took the one-launch path,
+    # which does not take cu_seqlens, and the call failed with nothing computed
+    print(f"batched B=1 {dtype} N={n} splits={splits}", flush=True)
+    q, c, cu = synthetic.batched_inputs(128, np.array([n]), seed=31 + n)
+    if dtype == "fp8":
+        c8 = torch.from_numpy(c.astype(np.float32) * np.float32(2.0)).to(torch.float8_e4m3fn)
+        cd = c8.float().double().numpy() * 0.5
+        out = capi.decode_split_batched_fp8(_t(q), c8.to(_dev()), 0.5, _t(cu), num_splits=splits)
+        ref = O.closed_form_batched(q, cd, cu)
+    elif dtype == "bf16":
+        qb, cb = torch.from_numpy(q.astype(np.float32)).bfloat16(), torch.from_numpy(c.astype(np.float32)).bfloat16()
+        out = capi.decode_split_batched_bf16(qb.to(_dev()), cb.to(_dev()), _t(cu), num_splits=splits)
+        ref = O.closed_form_batched(qb.double().numpy(), cb.double().numpy(), cu)
+    else:
+        out = capi.decode_split_batched_fp16(_t(q), _t(c), _t(cu), num_splits=splits)
+        ref = O.closed_form_batched(q, c, cu)
+    torch.cuda.synchronize()
+    _check16(out.float().cpu().numpy()[0], ref[0], f"B=1 {dtype} N={n} splits={splits}")
+
+
 def test_batched_all_empty():
     q, _, _ = synthetic.batched_inputs(16, np.array([1, 1]), seed=1)
     cu = np.zeros(3, np.int32)

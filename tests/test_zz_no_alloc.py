@@ -42,7 +42,7 @@ def test_noalloc_matches_workspace_entry_on_consecutive_calls(first, second):
         assert torch.equal(got, ref), f"n_h={n_h} N={n}: max diff {(got.float() - ref.float()).abs().max()}"
 
 
-def test_noalloc_requested_splits_and_rejection():
+def test_noalloc_requested_splits():
     dev = torch.device("cuda:0")
     q, c = synthetic.decode_inputs(128, 3000, seed=5)
     qd, cd = torch.from_numpy(q).to(dev), torch.from_numpy(c).to(dev)
@@ -51,9 +51,6 @@ def test_noalloc_requested_splits_and_rejection():
     ref = capi.decode_split_fp16(qd, cd, num_splits=7)
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
-    # 4096 heads x 256 splits of partials (about 1 GB) cannot fit the 32 MiB scratch:
-    # rejected before anything is launched
-    lib = capi.load()
-    st = lib.mla_decode_split_fp16_noalloc(qd.data_ptr(), cd.data_ptr(), got.data_ptr(), 4096, 65536, 256, None)
-    assert st == capi.STATUS_SCRATCH_EXCEEDED
-    assert b"scratch" in lib.mla_status_string(st)
+    # The rejection of plans whose partials exceed the scratch is a host-side check,
+    # tested on the CPU with pointers that are never dereferenced
+    # (tests/test_boundary_cpu.py): no call here claims sizes its buffers do not have.
