@@ -90,6 +90,21 @@ void set_chunks(Plan &p, int total_tokens, int batch, int w)
     p.xcd_remap = 1;
 }
 
+#ifndef MLA_PIECE_TOKENS_64
+#define MLA_PIECE_TOKENS_64 192
+#endif
+// Calls with cu_seqlens: what starting a piece (one sequence's part of a
+// chunk: its Q* and first blocks loaded, the pipeline filled, its partial
+// stored) costs, in tokens of steady-state work at each head tile. Chunks
+// are cut over a virtual length in which every sequence start counts this
+// many tokens, so a chunk that holds more pieces holds fewer tokens.
+// Measured at 64-head tiles (config 5, B = 32): chunks of one, two and
+// three pieces took 64, 71 and 76 us with equal token counts.
+int piece_cost_tokens(int head_tile)
+{
+    return head_tile == 64 ? MLA_PIECE_TOKENS_64 : head_tile == 32 ? 224 : 288;
+}
+
 // Fixed cost (us) of a one-launch call (one chunk, the split kernel writes
 // the output): the two-launch fixed cost below less the combine launch.
 constexpr double kDirectFixedUs = 7.0;
@@ -142,6 +157,7 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch, bool se
         p.n_chunks = 0;
         p.n_slots = batch;  // unused; keeps the workspace non-empty
         p.xcd_remap = 0;
+        p.seq_cost = 0;
         p.part_bytes = (fp32 || f32_partials) ? 4 : 2;
         return p;
     }
@@ -178,11 +194,17 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch, bool se
         c.block_tokens = 32;
         c.n_head_tiles = num_heads / ht;
         c.part_bytes = f32_partials ? 4 : 2;
-        int w_lo = 1, w_hi = std::max(1, std::min(cu_count / c.n_head_tiles, ceil_div(total_tokens, c.block_tokens)));
+        // with cu_seqlens the chunks split the virtual length (piece_cost_tokens)
+        // (plain token chunks if the virtual length would not fit an int)
+        c.seq_cost = seqlens ? piece_cost_tokens(ht) : 0;
+        if ((long long)total_tokens + (long long)c.seq_cost * batch > INT32_MAX / 2)
+            c.seq_cost = 0;
+        const int total_v = total_tokens + c.seq_cost * batch;
+        int w_lo = 1, w_hi = std::max(1, std::min(cu_count / c.n_head_tiles, ceil_div(total_v, c.block_tokens)));
         if (num_splits > 0)
             w_lo = w_hi = num_splits;
         for (int w = w_lo; w <= w_hi; ++w) {
-            set_chunks(c, total_tokens, batch, w);
+            set_chunks(c, total_v, batch, w);
             const double us = modelled_us(c, num_heads, total_tokens, batch, cu_count, paged,
                                           !seqlens && cache != CacheKind::kPaged);
             if (best_us == 0.0 || us < best_us) {
@@ -589,9 +611,18 @@ size_t mla_decode_split_fp8_workspace_size(int batch, int num_heads, int total_t
 {
     if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)
         return 0;
-    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, true, num_splits,
-                                       mla::current_cu_count(), mla::CacheKind::kF8);
-    return mla::partials_bytes(p, num_heads);
+    // one size for both fp8 entries: with batch 1 it also covers the
+    // single-sequence entry's plan (no cu_seqlens, so no piece costs)
+    const int cu = mla::current_cu_count();
+    const mla::Plan p = mla::make_plan(false, num_heads, total_tokens, batch, true, num_splits, cu,
+                                       mla::CacheKind::kF8);
+    size_t bytes = mla::partials_bytes(p, num_heads);
+    if (batch == 1) {
+        const mla::Plan q = mla::make_plan(false, num_heads, total_tokens, 1, false, num_splits, cu,
+                                           mla::CacheKind::kF8);
+        bytes = std::max(bytes, mla::partials_bytes(q, num_heads));
+    }
+    return bytes;
 }
 
 int mla_decode_split_batched_fp8(const void *query, const void *cache_fp8, float cache_scale,

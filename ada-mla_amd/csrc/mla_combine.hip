@@ -67,7 +67,7 @@ void combine_kernel(const PartT *__restrict__ o_part,
                     const float *__restrict__ l_part,
                     const int *__restrict__ cu_seqlens,
                     void *__restrict__ out,
-                    int num_heads, int total_tokens, int chunk, int n_items, int n_chunks)
+                    int num_heads, int total_tokens, int chunk, int n_items, int n_chunks, int seq_cost)
 {
     constexpr int kWaves = W > 8 ? W : 8;
     constexpr int kItems = kWaves / W;
@@ -99,8 +99,9 @@ void combine_kernel(const PartT *__restrict__ o_part,
         const int lo = min(max(cu_seqlens[b], 0), total_tokens);
         const int hi = min(max(cu_seqlens[b + 1], lo), total_tokens);
         if (hi > lo) {
-            s0 = lo / chunk + b;
-            ns = (hi - 1) / chunk + b - s0 + 1;
+            const long long c = (long long)seq_cost * (b + 1);  // virtual offset of the sequence
+            s0 = (int)((lo + c) / chunk) + b;
+            ns = (int)((hi - 1 + c) / chunk) + b - s0 + 1;
         }
     }
     const int head = (tile >> 5) * 16 + (lane & 15);
@@ -223,7 +224,7 @@ void combine_tiles_kernel(const PartT *__restrict__ o_part,
                           const float *__restrict__ l_part,
                           const int *__restrict__ cu_seqlens,
                           void *__restrict__ out,
-                          int num_heads, int total_tokens, int chunk, int n_groups)
+                          int num_heads, int total_tokens, int chunk, int n_groups, int seq_cost)
 {
     constexpr bool kNorm = !std::is_same<OutT, float>::value;
     using V = typename SlotBatch<PartT>::V;
@@ -255,8 +256,9 @@ void combine_tiles_kernel(const PartT *__restrict__ o_part,
     for (int t = 0; t < kT; ++t)
         acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (hi > lo) {
-        const int s0 = lo / chunk + b;
-        const int ns = (hi - 1) / chunk + b - s0 + 1;
+        const long long c = cu_seqlens ? (long long)seq_cost * (b + 1) : 0;  // virtual offset of the sequence
+        const int s0 = (int)((lo + c) / chunk) + b;
+        const int ns = (int)((hi - 1 + c) / chunk) + b - s0 + 1;
         const size_t slot_elems = (size_t)num_heads * kDV;
         const PartT *op = o_part + (size_t)s0 * slot_elems + (size_t)tile0 * 256 + lane * 4;
         const float *mp = m_part + (size_t)s0 * num_heads + head;
@@ -346,7 +348,8 @@ void launch_w(const Problem &pb, const Plan &p, const Partials &w, int n_items, 
     constexpr int kItems = kWaves / W;
     hipLaunchKernelGGL((combine_kernel<PartT, OutT, W>), dim3((n_items + kItems - 1) / kItems),
                        dim3(64 * kWaves), 0, s, static_cast<const PartT *>(w.o), w.m, w.l,
-                       pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk, n_items, p.n_chunks);
+                       pb.cu_seqlens, pb.out, pb.num_heads, pb.total_tokens, p.chunk, n_items, p.n_chunks,
+                       p.seq_cost);
 }
 
 template <typename PartT, typename OutT>
@@ -357,7 +360,7 @@ void launch_part(const Problem &pb, const Plan &p, const Partials &w, int waves,
         const int n_groups = n_items / kT;
         hipLaunchKernelGGL((combine_tiles_kernel<PartT, OutT>), dim3((n_groups + 3) / 4), dim3(256), 0, s,
                            static_cast<const PartT *>(w.o), w.m, w.l, pb.cu_seqlens, pb.out, pb.num_heads,
-                           pb.total_tokens, p.chunk, n_groups);
+                           pb.total_tokens, p.chunk, n_groups, p.seq_cost);
         return;
     }
     switch (waves) {

@@ -164,4 +164,39 @@ __host__ __device__ __forceinline__ size_t frag_offset(int head, int dim)
     return ((size_t)(head >> 4) * 32 + (dim >> 4)) * 256 + (((dim & 15) >> 2) * 16 + (head & 15)) * 4 + (dim & 3);
 }
 
+// Chunk bounds of a batch (cu_seqlens [batch + 1]), computed by one wave
+// (all 64 lanes active). Sequence b's tokens [cu[b], cu[b+1]) take the
+// virtual positions [cu[b] + seq_cost (b + 1), cu[b+1] + seq_cost (b + 1)):
+// every sequence start adds seq_cost virtual tokens, the measured cost of
+// starting a piece in tokens of steady-state work. Returns the first
+// sequence whose virtual end exceeds x (batch if none) and sets t to the
+// first real token at or after virtual position x (total if none), and
+// seq_lo / seq_hi to that sequence's bounds (total if none). cu_seqlens
+// entries are clamped as the kernels' piece walks clamp them.
+__device__ __forceinline__ int seq_virtual_bound(const int *cu, int batch, int total, int seq_cost, long long x,
+                                                 int lane, int &t, int &seq_lo, int &seq_hi)
+{
+    for (int base = 0; base < batch; base += 64) {
+        const int i = base + lane;
+        bool past = false;
+        int lo_i = 0, hi_i = 0;
+        if (i < batch) {
+            lo_i = min(max(cu[i], 0), total);
+            hi_i = min(max(cu[i + 1], lo_i), total);
+            past = (long long)hi_i + (long long)seq_cost * (i + 1) > x;
+        }
+        const unsigned long long m = __builtin_amdgcn_ballot_w64(past);
+        if (m != 0) {
+            const int k = __builtin_ctzll(m);
+            seq_lo = __builtin_amdgcn_readlane(lo_i, k);
+            seq_hi = __builtin_amdgcn_readlane(hi_i, k);
+            const long long v = x - (long long)seq_cost * (base + k + 1);
+            t = v > seq_lo ? (int)v : seq_lo;
+            return base + k;
+        }
+    }
+    t = seq_lo = seq_hi = total;
+    return batch;
+}
+
 }  // namespace mla

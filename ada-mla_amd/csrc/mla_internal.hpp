@@ -13,16 +13,20 @@ constexpr int kDV = 512;  // value width (C_N = C[:, :512])
 
 // Split-KV schedule. The packed token range [0, total_tokens) is cut into
 // n_chunks chunks of `chunk` tokens; workgroup (chunk w, head tile h) handles
-// heads [h * head_tile, +head_tile) over the tokens of chunk w. A chunk that
-// spans sequences b..b' emits one partial result per sequence; the partial of
-// (chunk w, sequence b) lives in slot w + b, so slots never collide and a
-// sequence's partials are the contiguous slots
-// [lo_b / chunk + b, (hi_b - 1) / chunk + b].
+// heads [h * head_tile, +head_tile) over the tokens of chunk w. With
+// cu_seqlens the cut is over virtual positions: token t of sequence b sits
+// at t + seq_cost (b + 1) and chunk w holds the tokens whose virtual
+// positions fall in [w chunk, (w + 1) chunk). A chunk that spans sequences
+// b..b' emits one partial result per sequence; the partial of (chunk w,
+// sequence b) lives in slot w + b, so slots never collide and a sequence's
+// partials are the contiguous slots
+// [(lo_b + c_b) / chunk + b, (hi_b - 1 + c_b) / chunk + b], c_b = seq_cost (b + 1).
 struct Plan {
     int head_tile;     // heads per workgroup
     int n_head_tiles;  // num_heads / head_tile
     int block_tokens;  // tokens per LDS block
-    int chunk;         // tokens per split (multiple of block_tokens)
+    int chunk;         // tokens per split (virtual tokens with cu_seqlens; a multiple of
+                       // block_tokens)
     int n_chunks;      // splits over the packed tokens
     int n_slots;       // partial-result slots: n_chunks + batch - 1
     int xcd_remap;     // 1: the head tiles of one chunk share an XCD; the grid then
@@ -33,6 +37,9 @@ struct Plan {
                        // kMergeDirect: one chunk, the split kernel writes the output itself
     int part_plain;    // 1: the 16-bit split kernel stores its partials with plain stores,
                        // 0: with nontemporal ones (see choose_part_plain)
+    int seq_cost;      // calls with cu_seqlens: virtual tokens each sequence start adds, so
+                       // that chunks of `chunk` virtual tokens carry equal work with their
+                       // piece starts (seq_virtual_bound in mla_device.hpp); 0 otherwise
 };
 
 constexpr int kMergeCombine = 0;

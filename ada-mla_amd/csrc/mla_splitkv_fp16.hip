@@ -129,7 +129,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                          float *__restrict__ m_part,
                          float *__restrict__ l_part,
                          float scale_log2, Paging pg,
-                         float out_scale, E *__restrict__ out, int part_plain)
+                         float out_scale, E *__restrict__ out, int part_plain, int seq_cost)
 {
     using T = F16Tile<HT>;
     constexpr bool kDirect = kMode == kModeDirect;
@@ -175,32 +175,37 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             ht = bid - split * n_head_tiles;
         }
     }
-    if ((long long)split * chunk >= total_tokens)  // a padding workgroup of the grid
-        return;
-    const int lo = split * chunk;
-    const int hi = min(lo + chunk, total_tokens);
-    const int head0 = ht * HT;
-
-    // First sequence containing token lo (largest b with cu[b] <= lo).
-    int b_first = 0;
+    // The chunk's tokens [lo, hi). A batch is chunked over its virtual
+    // length (seq_virtual_bound): chunk w covers virtual positions
+    // [w chunk, (w + 1) chunk), every sequence start counting seq_cost
+    // tokens, so that chunks holding more pieces hold fewer tokens.
+    // b_first: the first sequence with tokens at or after lo.
+    int lo, hi, b_first = 0;
+    int first_lo = 0, first_hi = 0;  // bounds of sequence b_first
     const int nseq = cu_seqlens ? batch : 1;
     if (cu_seqlens) {
-        int l = 0, r = batch;
-        while (r - l > 1) {
-            const int mid = (l + r) >> 1;
-            if (cu_seqlens[mid] <= lo) l = mid; else r = mid;
-        }
-        b_first = l;
+        b_first = seq_virtual_bound(cu_seqlens, batch, total_tokens, seq_cost, (long long)split * chunk, lane, lo,
+                                    first_lo, first_hi);
+        int u0, u1;
+        seq_virtual_bound(cu_seqlens, batch, total_tokens, seq_cost, (long long)(split + 1) * chunk, lane, hi, u0, u1);
+        if (lo >= hi)  // a padding workgroup, or a chunk that falls between sequences
+            return;
+    } else {
+        if ((long long)split * chunk >= total_tokens)  // a padding workgroup of the grid
+            return;
+        lo = split * chunk;
+        hi = min(lo + chunk, total_tokens);
     }
+    const int head0 = ht * HT;
     // Calls body(b, seq_lo, p_org, p_lo, p_hi) for every non-empty piece
     // [p_lo, p_hi) of sequence b (whose first token is seq_lo) inside this
     // chunk. Blocks of the piece start at p_org: p_lo itself, or, for a paged
     // cache, p_lo rounded down to a multiple of 32 tokens of the sequence, so
     // that no block straddles a page (tokens before p_lo are masked). Every
     // wave walks the same pieces and, per piece, passes the same number of
-    // barriers (nblk + 5; nblk + 4 for a single sequence, whose prologue
-    // loads need no piece-start barrier; one more with an fp8 cache and
-    // 32 or 64 heads, before the split of Q*).
+    // barriers (nblk + 5; nblk + 4 for the chunk's first piece, whose
+    // prologue loads go out at kernel entry and need no piece-start barrier;
+    // one more with an fp8 cache and 32 or 64 heads, before the split of Q*).
     auto for_each_piece = [&](auto &&body) {
         for (int b = b_first; b < nseq; ++b) {
             int seq_lo = 0, seq_hi = total_tokens;
@@ -404,13 +409,21 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     // waves take ~0.5-0.8 us to reach the first barrier (measured), which
     // the loads now overlap (same box, N = 4096: 11.85 -> 11.64 us per call;
     // n_h = 16: 16.8 -> 16.3 us). Batches issue every piece's loads after the
-    // piece-start barrier, once the ring is free (piece_prologue): their
-    // first piece also needs the sequence bounds, scalar loads that the
-    // early issue would wait for (batched was 1.7% slower with it).
+    // piece-start barrier, once the ring is free (piece_prologue), except
+    // for the chunk's first piece, whose bounds the sequence search at entry
+    // already found.
     int first_b = -1;
     if constexpr (kMode != kModeBatch) {
         first_b = 0;
         prologue_issue(0, 0, lo, hi);
+    } else if (cu_seqlens) {
+        // a batch's first piece: its bounds came with the chunk's (the
+        // sequence search), so its loads go out now as well
+        const int p_hi0 = min(first_hi, hi);
+        if (b_first < batch && lo < p_hi0) {
+            first_b = b_first;
+            prologue_issue(b_first, first_lo, kPaged ? lo - ((lo - first_lo) & (T::kBT - 1)) : lo, p_hi0);
+        }
     }
     // fp8 cache: the first product runs on fp8 MFMAs with Q* split into
     // two fp8 operands, so that C is used as stored (no conversion of the
@@ -1275,7 +1288,7 @@ hipError_t launch_ht(const Problem &pb, const Plan &p, const Partials &w, hipStr
     hipLaunchKernelGGL((splitkv_fp16_kernel<HT, kTr, E, kPaged, kF32Part, kF8, kMode>), grid, block, 0, s,
                        (const E *)pb.q, (const E *)pb.c, pb.cu_seqlens, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, w.o, w.m, w.l, pb.scale_log2, pb.paging, pb.out_scale,
-                       (E *)pb.out, p.part_plain);
+                       (E *)pb.out, p.part_plain, p.seq_cost);
     // the launch's own error; hipPeekAtLastError leaves a sticky error from
     // the caller's earlier work in place for the caller to see
     return hipPeekAtLastError();

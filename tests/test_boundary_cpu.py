@@ -344,3 +344,23 @@ def test_batched_single_sequence_reaches_the_launch(fn, splits):
     args = (FAKE, FAKE) + ((1.0,) if fn.endswith("fp8") else ()) + (FAKE, FAKE, FAKE, 1 << 30, 1, 128, 100, splits, None)
     assert f(*args) == capi.STATUS_HIP_ERROR
     assert lib.mla_last_hip_error() != 1  # not hipErrorInvalidValue from the plan/launch mismatch
+
+
+@pytest.mark.parametrize("n", [1, 100, 1000, 4097, 65536])
+def test_fp8_workspace_size_covers_the_single_sequence_entry(n):
+    # mla_decode_split_fp8_workspace_size serves both fp8 entries; with batch 1
+    # it must also cover the single-sequence entry's plan, which (no
+    # cu_seqlens) may cut the sequence differently from a batch of one.
+    # Without a GPU a call with enough workspace fails only at the launch.
+    if torch.cuda.device_count() > 0:
+        pytest.skip("launch-reaching CPU check: needs a machine without a GPU")
+    lib = capi.load()
+    ws = lib.mla_decode_split_fp8_workspace_size(1, 128, n, 0)
+    for flagless_splits in (0, 3):
+        ws_s = lib.mla_decode_split_fp8_workspace_size(1, 128, n, flagless_splits)
+        st = lib.mla_decode_split_fp8(FAKE, FAKE, 1.0, FAKE, FAKE, ws_s, 128, n, flagless_splits, None)
+        assert st == capi.STATUS_HIP_ERROR, (n, flagless_splits, st)
+        st = lib.mla_decode_split_batched_fp8(FAKE, FAKE, 1.0, FAKE, FAKE, FAKE, ws_s, 1, 128, n, flagless_splits,
+                                              None)
+        assert st == capi.STATUS_HIP_ERROR, (n, flagless_splits, st)
+    assert ws > 0

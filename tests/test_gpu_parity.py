@@ -302,15 +302,36 @@ def test_batched_many_items_with_empty(n_h, batch, splits):
 MANY_PIECES = np.array([130, 200, 0, 150, 300, 129, 40, 260, 140, 0, 500, 97, 1000, 33, 160, 128, 1, 255])
 
 
+# Piece costs the planner may charge per sequence start (virtual tokens, by
+# head tile); chunks cut the virtual length (token t of sequence b at
+# t + cost (b + 1)) into equal parts.
+PIECE_COSTS = (192, 224, 288)
+
+
+def _chunk_bounds(seqlens, splits, cost):
+    """Real token ranges of the chunks of a requested split count: a
+    restatement of the planner's chunking and the kernel's virtual bounds."""
+    cu = np.concatenate([[0], np.cumsum(seqlens)])
+    total_v = int(cu[-1]) + cost * len(seqlens)
+    chunk = -(-(-(-total_v // splits)) // 32) * 32
+
+    def real(x):  # first real token at or after virtual position x
+        for b in range(len(seqlens)):
+            if cu[b + 1] + cost * (b + 1) > x:
+                return max(int(cu[b]), x - cost * (b + 1))
+        return int(cu[-1])
+    return [(real(v), real(v + chunk)) for v in range(0, total_v, chunk)]
+
+
 def _max_pieces_per_chunk(seqlens, splits):
     cu = np.concatenate([[0], np.cumsum(seqlens)])
-    total = int(cu[-1])
-    chunk = -(-(-(-total // splits)) // 32) * 32
-    most = 0
-    for lo in range(0, total, chunk):
-        hi = min(lo + chunk, total)
-        most = max(most, sum(1 for b in range(len(seqlens)) if max(cu[b], lo) < min(cu[b + 1], hi)))
-    return most
+    most = []
+    for cost in PIECE_COSTS:
+        m = 0
+        for lo, hi in _chunk_bounds(seqlens, splits, cost):
+            m = max(m, sum(1 for b in range(len(seqlens)) if max(cu[b], lo) < min(cu[b + 1], hi)))
+        most.append(m)
+    return min(most)
 
 
 @pytest.mark.parametrize("n_h", [16, 32, 64, 128])
@@ -322,6 +343,32 @@ def test_batched_chunks_spanning_many_pieces(n_h, splits):
     got = _batched(q, c, cu, num_splits=splits)
     ref = O.closed_form_batched(q, c, cu)
     for b, n in enumerate(MANY_PIECES):
+        if n == 0:
+            assert not got[b].any(), f"empty seq {b}"
+        else:
+            _check16(got[b], ref[b], f"seq {b} N={n}")
+
+
+@pytest.mark.parametrize("case,splits", [("gaps", 40), ("gaps", 0), ("wide", 0), ("wide", 150), ("wide", 7)])
+def test_batched_virtual_chunks(case, splits):
+    # Chunks cut a batch's virtual length, in which every sequence start adds
+    # the planner's piece cost. "gaps": short sequences among empty ones with
+    # many requested splits, so that some chunks fall between sequences and
+    # hold no tokens; "wide": more than 64 sequences (the sequence search
+    # runs over cu_seqlens in passes of 64), ragged, with empty ones.
+    if case == "gaps":
+        seqlens = np.array([5, 0, 0, 0, 7, 3, 0, 40, 0, 1])
+        assert all(any(lo >= hi for lo, hi in _chunk_bounds(seqlens, 40, c)) for c in PIECE_COSTS)
+    else:
+        rng = np.random.default_rng(77)
+        seqlens = rng.integers(1, 600, size=150)
+        seqlens[::9] = 0
+        seqlens[70] = 3000
+    print(f"virtual chunks {case} splits={splits}", flush=True)
+    q, c, cu = synthetic.batched_inputs(32, seqlens, seed=13)
+    got = _batched(q, c, cu, num_splits=splits)
+    ref = O.closed_form_batched(q, c, cu)
+    for b, n in enumerate(seqlens):
         if n == 0:
             assert not got[b].any(), f"empty seq {b}"
         else:
