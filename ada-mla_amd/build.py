@@ -7,7 +7,8 @@
 
 The .hip sources are compiled by hipcc directly (not through
 torch.utils.cpp_extension, which would run hipify on them). Objects go to
-ada-mla_amd/_build/ (git-ignored). Usage: python ada-mla_amd/build.py [--lib-only]
+ada-mla_amd/_build/ (git-ignored). Usage: python ada-mla_amd/build.py [--lib-only | --timeline]
+(--timeline: only the instrumented ada_mla/libmla_mi355x_timeline.so, see build_lib)
 """
 from __future__ import annotations
 
@@ -29,6 +30,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIP_SOURCES = ["mla_splitkv_fp16.hip", "mla_splitkv_fp32.hip", "mla_combine.hip", "mla_capi.hip",
                "mla_block.hip"]
 LIB_NAME = "libmla_mi355x.so"
+TIMELINE_LIB_NAME = "libmla_mi355x_timeline.so"
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -55,20 +57,26 @@ def _run(cmd):
     return out
 
 
-def build_lib(jobs: int = 4) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+def build_lib(jobs: int = 4, timeline: bool = False) -> str:
+    """The library; with timeline=True the instrumented copy
+    ada_mla/libmla_mi355x_timeline.so (-DMLA_TIMELINE: the split kernel records
+    per-workgroup phase stamps, read by ada-mla_amd/timeline.py), which
+    nothing else loads."""
+    build_dir = os.path.join(BUILD, "timeline") if timeline else BUILD
+    os.makedirs(build_dir, exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     objs = []
     cmds = []
+    extra = ["-DMLA_TIMELINE"] if timeline else []
     for src in HIP_SOURCES:
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIPCC_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         for out in ex.map(_run, cmds):
             if out.strip():
                 print(out)
-    lib = os.path.join(OUT_DIR, LIB_NAME)
+    lib = os.path.join(OUT_DIR, TIMELINE_LIB_NAME if timeline else LIB_NAME)
     tmp = lib + ".tmp"
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, lib)
@@ -96,7 +104,10 @@ def build_ext() -> str:
     return target
 
 
-def build(lib_only: bool = False) -> None:
+def build(lib_only: bool = False, timeline: bool = False) -> None:
+    if timeline:
+        print(f"built {os.path.relpath(build_lib(timeline=True), REPO)}")
+        return
     lib = build_lib()
     print(f"built {os.path.relpath(lib, REPO)}")
     if not lib_only:
@@ -105,4 +116,4 @@ def build(lib_only: bool = False) -> None:
 
 
 if __name__ == "__main__":
-    build(lib_only="--lib-only" in sys.argv)
+    build(lib_only="--lib-only" in sys.argv, timeline="--timeline" in sys.argv)

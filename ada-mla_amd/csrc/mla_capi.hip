@@ -7,6 +7,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <mutex>
 
 #include "mla_internal.hpp"
@@ -189,6 +190,11 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch, bool se
     for (int ht : {64, 32, 16}) {
         if (num_heads % ht != 0)
             continue;
+#ifdef MLA_TIMELINE
+        // timeline build only (ada-mla_amd/timeline.py): MLA_TIMELINE_HEAD_TILE pins the tile
+        if (const char *e = std::getenv("MLA_TIMELINE_HEAD_TILE"); e && std::atoi(e) != ht)
+            continue;
+#endif
         Plan c{};
         c.head_tile = ht;
         c.block_tokens = 32;

@@ -9,9 +9,9 @@
 //
 // Replaces mla_decode_splitk_mma_fp16 (reference
 // csrc/mla_decode_splitk_fwd.cuh:559-892), with a different design:
-//  * 512 threads = 8 wave64s, one workgroup per CU, in two roles with one
-//    wave of each role on every SIMD, so that one role's LDS and softmax
-//    latencies hide behind the other role's MFMAs:
+//  * 512 threads = 8 wave64s (640 = 10 at 32-head tiles), one workgroup per
+//    CU, in two roles with one wave of each role on every SIMD, so that one
+//    role's LDS and softmax latencies hide behind the other role's MFMAs:
 //      - S waves compute the logits and the online softmax of block t+1:
 //        S^T = C Q*^T on 16x16x32 MFMAs over the full K = 576. Wave
 //        (head group, token half) owns up to 32 heads x 16 tokens of each
@@ -27,9 +27,10 @@
 //        of the two halves' running maxima, scale each half's P by
 //        2^(m_half - M) and the accumulator by 2^(M_old - M).
 //      - the ring is fed (global->LDS loads) by the O waves, between their
-//        MFMAs, when the head tile is 64; for tiles of 16 or 32 heads two
-//        S waves suffice and waves 2 and 3 only feed the ring, which keeps
-//        the load-issue stalls off the O waves.
+//        MFMAs, when the head tile is 64; for tiles of 16 heads two S waves
+//        suffice and waves 2 and 3 only feed the ring, which keeps the
+//        load-issue stalls off the O waves; tiles of 32 heads run four
+//        16-head S waves and two more waves, 8 and 9, that feed.
 //    P (fp16) and the halves' maxima pass from S to O waves through a
 //    double-buffered LDS area; one workgroup barrier per block.
 //  * C streams through a 4-slot LDS ring of 32-token blocks filled by
@@ -62,15 +63,46 @@
 #include "mla_ring.hpp"
 
 namespace mla {
+
+#ifdef MLA_TIMELINE
+// Timeline build only (python ada-mla_amd/build.py --timeline, read by
+// ada-mla_amd/timeline.py through mla_timeline_read): per workgroup, 16
+// stamps of its last piece -- s_memrealtime (100 MHz, one clock for the whole
+// GPU) at the phase boundaries of wave 0 (an S wave) and wave 4 (an O wave),
+// s_memtime (shader clock) around both waves' block loops, the piece's block
+// count and the hardware ids. The normal build compiles none of it.
+constexpr int kTimelineWorkgroups = 8192;
+__device__ unsigned long long mla_timeline_stamps[kTimelineWorkgroups * 16];
+#define MLA_STAMP(w, e, v)                                                              \
+    do {                                                                               \
+        if (wave == (w) && lane == 0 && blockIdx.x < kTimelineWorkgroups)              \
+            mla_timeline_stamps[blockIdx.x * 16 + (e)] = (unsigned long long)(v);      \
+    } while (0)
+#define MLA_RT() __builtin_amdgcn_s_memrealtime()
+#define MLA_MT() __builtin_amdgcn_s_memtime()
+#else
+#define MLA_STAMP(w, e, v) \
+    do {                   \
+    } while (0)
+#endif
+
 namespace {
 
 template <int HT>
 struct F16Tile {
-    static constexpr int kWaves = 8;
+    // kTen: 32-head tiles run 10 waves -- four 16-head S waves (head group,
+    // token half), four O waves and two dedicated feeders (waves 8 and 9),
+    // three waves on SIMDs 0 and 1 (at most 168 registers each). With two
+    // 32-head S waves (8 waves) the first product and the softmax of a block
+    // ran on SIMDs 0 and 1 only; split over four SIMDs the step went from
+    // 1630 to 1283 cycles at N = 65536 (the clock fell from 2.0 to 1.86 GHz:
+    // 0.815 -> 0.696 us) and the split kernel from 30.0 to 28.8 us (same box).
+    static constexpr bool kTen = HT == 32;
+    static constexpr int kWaves = kTen ? 10 : 8;
     static constexpr int kThreads = 64 * kWaves;
     static constexpr int kBT = 32;                      // tokens per block
     static constexpr int kRing = 4;                     // LDS ring slots
-    static constexpr int kSH = HT < 32 ? HT : 32;       // heads per S wave
+    static constexpr int kSH = kTen ? 16 : HT < 32 ? HT : 32;  // heads per S wave
     static constexpr int kNS = kSH / 16;                // 16-head sub-tiles per S wave
     static constexpr int kNHG = HT / kSH;               // head groups
     static constexpr int kSWaves = 2 * kNHG;            // S waves: (head group, token half)
@@ -87,12 +119,13 @@ struct F16Tile {
     static constexpr int kPre = kRing - kQBlocks;       // blocks issued with Q*
     // Feeding of the ring (global -> LDS): the O waves at HT = 64, else the
     // two waves after the S waves; each feeder owns kFeedRows rows of a block.
-    static constexpr bool kOFeeds = kSWaves == kOWave0;
+    static constexpr bool kOFeeds = !kTen && kSWaves == kOWave0;
+    static constexpr int kFeedWave0 = kOFeeds ? kOWave0 : kTen ? 8 : kSWaves;  // first feeder wave
     static constexpr int kFeeders = kOFeeds ? 4 : 2;
     static constexpr int kFeedRows = kBT / kFeeders;
     static constexpr int kFeedUnits = kFeedRows + kFeedRows / 8;  // C_N rows + rope units
     static_assert(kFeeders * kFeedUnits == kUnits, "feeder split");
-    static_assert(kOFeeds || kSWaves == 2, "feeder waves are 2 and 3");
+    static_assert(kOFeeds || kSWaves == 2 || kTen, "feeder waves are 2 and 3 (8 and 9 with kTen)");
     static_assert(3 * kFeedUnits <= 63, "vmcnt range");
 };
 
@@ -116,7 +149,8 @@ constexpr int kModeSingle = 1;
 constexpr int kModeDirect = 2;
 
 template <int HT, bool kTr, typename E, bool kPaged, bool kF32Part, bool kF8, int kMode>
-__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(F16Tile<HT>::kThreads, F16Tile<HT>::kThreads),
+                          amdgpu_waves_per_eu(F16Tile<HT>::kWaves > 8 ? 3 : 2, F16Tile<HT>::kWaves > 8 ? 3 : 2)))
 // Arguments: what the workgroup mapping and a single sequence's entry loads
 // need come first, within the 16 dwords preloaded into SGPRs at wave launch
 // (the library is built with -amdgpu-kernarg-preload-count=16).
@@ -156,6 +190,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15;
     const int g = lane >> 4;
+    MLA_STAMP(0, 0, MLA_RT());
 
     // workgroup -> (chunk, head tile). With xcd_remap the head tiles of one
     // chunk get ids that are equal mod 8, i.e. land on the same XCD (blocks
@@ -373,7 +408,10 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     // own loads of Q* and block 0 only (prologue_own_wait); the barrier after
     // this (A) then publishes them to every wave, and blocks 1..kPre-1 land
     // while block 0 is computed (prologue_wait, and the feeders' first wait).
+    // (waves 8 and 9 of a 10-wave tile, dedicated feeders, issue none)
     auto prologue_issue = [&](int b, int seq_lo, int p_org, int p_hi) {
+        if (T::kWaves > 8 && wave >= 8)
+            return;
         const E *qb = q + ((size_t)b * num_heads + head0) * kDK;
 #pragma unroll
         for (int j = 0; j < T::kQBlocks; ++j) {
@@ -401,7 +439,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
     auto prologue_own_wait = [&]() {
         if (wave < 4)
             MLA_WAIT_VMCNT(5 * (T::kPre - 1));
-        else
+        else if (T::kWaves == 8 || wave < 8)
             MLA_WAIT_VMCNT(4 * (T::kPre - 1));
     };
     // A single sequence's prologue loads (its chunk is one piece, [lo, hi))
@@ -573,10 +611,11 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             // while the piece's first blocks arrive
             if (wave < 4)
                 MLA_WAIT_VMCNT(5 * T::kPre);
-            else
+            else if (T::kWaves == 8 || wave < 8)
                 MLA_WAIT_VMCNT(4 * T::kPre);
             lds_barrier();  // Q* has landed
-            q_split_lds();
+            if (T::kWaves == 8 || wave < 8)
+                q_split_lds();
         }
         prologue_own_wait();
     };
@@ -643,7 +682,9 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             const int slot_out = split + b;
             const int nblk = (p_hi - p_org + T::kBT - 1) / T::kBT;
             piece_prologue(b, seq_lo, p_org, p_hi);
+            MLA_STAMP(0, 1, MLA_RT());
             lds_barrier();  // A: Q* (split, with kF8M) and block 0 have landed
+            MLA_STAMP(0, 2, MLA_RT());
             // Q* fragments (B operand of S^T = C Q*^T): lane holds head
             // kSH*hg + 16*ns + l16 of the tile, dims 32*kk + 8*g .. +7. Q*
             // rows sit in the ring in the same swizzled layout as C rows.
@@ -696,6 +737,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 }
             }
             lds_barrier();  // B: the Q* slots are free again
+            MLA_STAMP(0, 3, MLA_RT());
+            MLA_STAMP(0, 6, MLA_MT());
 
             float m_run[T::kNS], l_lane[T::kNS];  // running max (uniform over g); per-lane partial sum
 #pragma unroll
@@ -872,6 +915,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     prologue_wait(t);
                 lds_barrier();
             }
+            MLA_STAMP(0, 4, MLA_RT());
+            MLA_STAMP(0, 7, MLA_MT());
             // ---- epilogue: this half's running max and sum per head; the
             // first half merges both and writes the piece's m and l (the
             // LDS addresses formed here from an opaque copy of the lane, not
@@ -907,6 +952,10 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                     }
                 }
             }
+#ifdef MLA_TIMELINE
+            MLA_WAIT_VMCNT(0);
+#endif
+            MLA_STAMP(0, 5, MLA_RT());
         });
     } else {
         // ---- global -> LDS feeding of the ring. kFeeders waves share each
@@ -916,7 +965,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         // for the rope part (lane -> row 8*ru + lane/8, stored position
         // lane % 8). The O waves feed at HT = 64; otherwise waves 2 and 3,
         // which have no other role, do.
-        const int feeder = T::kOFeeds ? wave - T::kOWave0 : wave - T::kSWaves;
+        const int feeder = wave - T::kFeedWave0;
         // fp8: 64-lane units of two C_N rows (and, with the 16 rows of a
         // dedicated feeder, of 16 rope rows), about half the load
         // instructions per block
@@ -965,8 +1014,10 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             if (t < 0) {
                 if (wave < 4)
                     MLA_WAIT_VMCNT(5 * (T::kPre - 2) + (T::kRing - T::kPre) * kFU);
-                else
+                else if (T::kWaves == 8 || wave < 8)
                     MLA_WAIT_VMCNT(4 * (T::kPre - 2) + (T::kRing - T::kPre) * kFU);
+                else  // no prologue loads of its own
+                    MLA_WAIT_VMCNT((T::kRing - T::kPre) * kFU);
             } else if (issued) {
                 MLA_WAIT_VMCNT(2 * kFU);
             } else {
@@ -974,7 +1025,7 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             }
         };
 
-        if (wave >= T::kOWave0) {
+        if (wave >= T::kOWave0 && wave < T::kOWave0 + 4) {
             const int ow = wave - T::kOWave0;  // column quarter
             // When the O waves also feed the ring (HT = 64) they carry the
             // step: they issue first when both waves of a SIMD are ready, so
@@ -1052,6 +1103,9 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                 }
                 lds_barrier();  // A
                 lds_barrier();  // B
+                MLA_STAMP(4, 8, MLA_RT());
+                MLA_STAMP(4, 12, MLA_MT());
+                MLA_STAMP(4, 11, nblk);
                 if constexpr (T::kOFeeds) {
 #pragma unroll
                     for (int blk = T::kPre; blk < T::kRing; ++blk) {
@@ -1190,6 +1244,8 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         prologue_wait(t);
                     lds_barrier();
                 }
+                MLA_STAMP(4, 9, MLA_RT());
+                MLA_STAMP(4, 13, MLA_MT());
                 if (g == 0) {
 #pragma unroll
                     for (int hs = 0; hs < T::kNHS; ++hs)
@@ -1235,6 +1291,10 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
                         }
                     }
                 }
+#ifdef MLA_TIMELINE
+                MLA_WAIT_VMCNT(0);
+#endif
+                MLA_STAMP(4, 10, MLA_RT());
             });
         } else {
             // dedicated feeder waves (head tiles of 16 or 32 heads)
@@ -1307,6 +1367,14 @@ hipError_t launch_tiles(const Problem &pb, const Plan &p, const Partials &w, hip
 }
 
 }  // namespace
+
+#ifdef MLA_TIMELINE
+extern "C" int mla_timeline_read(void *dst, size_t bytes)
+{
+    const size_t n = bytes < sizeof(mla_timeline_stamps) ? bytes : sizeof(mla_timeline_stamps);
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(mla_timeline_stamps), n, 0, hipMemcpyDeviceToHost);
+}
+#endif
 
 hipError_t launch_splitkv_fp16(const Problem &pb, const Plan &p, const Partials &w,
                                bool tr_load, hipStream_t s)

@@ -1,0 +1,159 @@
+"""Per-workgroup timeline of the fp16 split kernel on the GPU.
+
+Loads ada_mla/libmla_mi355x_timeline.so (python ada-mla_amd/build.py
+--timeline: the library built with -DMLA_TIMELINE, in which every workgroup
+of the split kernel records the phase boundaries of its last piece) and, for
+each case, after a 1 s spin-up, times K back-to-back split-kernel launches
+(mla_decode_split_fp16_partials: the split kernel alone) between two HIP
+events and reads the stamps of the last launch. Times are s_memrealtime
+(100 MHz, one clock for the whole GPU) relative to the first workgroup's
+entry; the shader clock is s_memtime cycles over s_memrealtime time around
+the block loop.
+
+Phases (median / min / max over the workgroups, us):
+  entry      wave 0 starts
+  landed     wave 0's own prologue loads (Q* rows, block 0) have landed
+  barrier_a  every wave's have: the block loop can start
+  barrier_b  the S waves hold Q* in registers
+  loop_end   the last block step ends (S and O waves)
+  s_done     the S waves' m and l are stored (stores complete)
+  o_done     the O waves' partial O is stored (stores complete)
+  step       (loop_end - barrier_b) / (blocks + 1): one block step
+
+A sweep over the sequence length at a fixed split count (--sweep) gives the
+step cost with every CU busy as the slope of the launch time over blocks per
+workgroup, and the fixed cost per launch as its intercept.
+
+Usage (single sequences, inputs rotated over >= 1 GB so that C comes from HBM):
+  python ada-mla_amd/timeline.py --heads 128 --tokens 65536 --splits 128 --head-tile 64
+  python ada-mla_amd/timeline.py --heads 128 --tokens 16384,32768,65536,131072 --splits 128 --head-tile 64 --sweep
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "ada_mla", "libmla_mi355x_timeline.so")
+SLOTS = 16
+FLAG_FP32_PARTIALS = 4
+NAMES = [("entry", 0), ("landed", 1), ("barrier_a", 2), ("barrier_b", 3), ("loop_end", 4), ("s_done", 5),
+         ("o_done", 10)]
+
+
+def run_case(lib, torch, n_h, n, splits, flags, k, spin_s):
+    vp = ctypes.c_void_p
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = vp(stream.cuda_stream)
+    set_bytes = n * 576 * 2 + n_h * 576 * 2
+    pool = min(64, max(2, math.ceil(1024 * 2**20 / set_bytes) + 1))
+    qs = [torch.randn(n_h, 576, device=dev, dtype=torch.float16) for _ in range(pool)]
+    cs = [torch.randn(n, 576, device=dev, dtype=torch.float16) for _ in range(pool)]
+    wsb = lib.mla_decode_split_workspace_size(n_h, n, splits)
+    if wsb == 0:
+        raise SystemExit(f"invalid sizes: heads {n_h}, tokens {n}, splits {splits}")
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    ht = lib.mla_decode_split_head_tile(n_h, n, splits, flags)
+    ns = lib.mla_decode_split_num_splits(n_h, n, splits, flags)
+    n_wg = ((ns + 7) // 8 * 8) * (n_h // ht)
+    cursor = [0]
+
+    def launch():
+        i = cursor[0] % pool
+        cursor[0] += 1
+        st = lib.mla_decode_split_fp16_partials(qs[i].data_ptr(), cs[i].data_ptr(), ws.data_ptr(), wsb, n_h, n,
+                                                splits, flags, sp)
+        if st != 0:
+            raise RuntimeError(f"mla_decode_split_fp16_partials: status {st}")
+
+    t_end = time.perf_counter() + spin_s
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            launch()
+        torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(k):
+        launch()
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000.0 / k
+    import numpy as np
+    buf = np.zeros(n_wg * SLOTS, dtype=np.uint64)
+    if lib.mla_timeline_read(buf.ctypes.data, buf.nbytes) != 0:
+        raise RuntimeError("mla_timeline_read failed")
+    x = buf.reshape(n_wg, SLOTS).astype(np.int64)
+    # padding workgroups of the grid stamp their entry only (their other
+    # slots keep an earlier launch's stamps)
+    x = x[x[:, 10] > x[:, 0]]
+    t0 = x[:, 0].min()
+    phases = {}
+    for name, e in NAMES:
+        v = (x[:, e] - t0) * 0.01
+        phases[name] = [round(float(np.median(v)), 2), round(float(v.min()), 2), round(float(v.max()), 2)]
+    nblk = x[:, 11]
+    steps = nblk + 1
+    loop_rt = (x[:, 9] - x[:, 8]) * 0.01
+    cyc = (x[:, 13] - x[:, 12]).astype(np.float64)
+    clk = float(np.median(cyc / (loop_rt * 1e3)))
+    step_us = float(np.median(((x[:, 4] - x[:, 3]) * 0.01) / steps))
+    rec = dict(heads=n_h, tokens=n, head_tile=int(ht), splits=int(ns), workgroups=int(len(x)),
+               blocks=int(np.median(nblk)), partials="fp32" if flags & FLAG_FP32_PARTIALS else "fp16",
+               launch_us=round(us, 2), span_us=round(float((x[:, 10].max() - t0) * 0.01), 2),
+               step_us=round(step_us, 3), step_cycles=round(float(np.median(cyc / steps))), clock_ghz=round(clk, 3),
+               phases_med_min_max_us=phases)
+    del qs, cs, ws
+    torch.cuda.empty_cache()
+    return rec
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--heads", type=int, default=128)
+    ap.add_argument("--tokens", default="4096", help="comma-separated sequence lengths")
+    ap.add_argument("--splits", type=int, default=0, help="split count (0: the planner's)")
+    ap.add_argument("--head-tile", type=int, default=0, choices=(0, 16, 32, 64), help="0: the planner's")
+    ap.add_argument("--partials", choices=("fp16", "fp32"), default="fp16")
+    ap.add_argument("--sweep", action="store_true", help="fit launch time = fixed + blocks x step")
+    ap.add_argument("--calls", type=int, default=20)
+    ap.add_argument("--spin-s", type=float, default=1.0)
+    args = ap.parse_args()
+    if not os.path.exists(LIB):
+        raise SystemExit(f"{LIB} is not built (python ada-mla_amd/build.py --timeline)")
+    if args.head_tile:
+        os.environ["MLA_TIMELINE_HEAD_TILE"] = str(args.head_tile)
+    import torch
+    vp, sz, i_, u_ = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint
+    lib = ctypes.CDLL(LIB)
+    lib.mla_decode_split_workspace_size.restype = sz
+    lib.mla_decode_split_workspace_size.argtypes = [i_, i_, i_]
+    lib.mla_decode_split_fp16_partials.argtypes = [vp, vp, vp, sz, i_, i_, i_, u_, vp]
+    lib.mla_decode_split_head_tile.argtypes = [i_, i_, i_, u_]
+    lib.mla_decode_split_num_splits.argtypes = [i_, i_, i_, u_]
+    lib.mla_timeline_read.argtypes = [vp, sz]
+    flags = FLAG_FP32_PARTIALS if args.partials == "fp32" else 0
+    recs = []
+    for n in (int(t) for t in args.tokens.split(",")):
+        rec = run_case(lib, torch, args.heads, n, args.splits, flags, args.calls, args.spin_s)
+        print(json.dumps(rec), flush=True)
+        recs.append(rec)
+    if args.sweep and len(recs) >= 2:
+        import numpy as np
+        xb = np.array([r["blocks"] for r in recs], dtype=np.float64)
+        yt = np.array([r["launch_us"] for r in recs])
+        slope, icpt = np.polyfit(xb, yt, 1)
+        print(json.dumps(dict(fit="launch_us = fixed_us + blocks x step_us", step_us=round(float(slope), 3),
+                              fixed_us=round(float(icpt), 2), head_tile=recs[0]["head_tile"],
+                              splits=recs[0]["splits"], partials=recs[0]["partials"])), flush=True)
+
+
+if __name__ == "__main__":
+    sys.exit(main())
