@@ -16,7 +16,14 @@
 //    LDS read and feeds them to 4 MFMAs (the same K permutation on A and B).
 //  * every wave then redoes the (tiny) softmax of the 16x16 tile, so all of
 //    them hold the running max and sum; wave 0 publishes P.
-//  * O^T = C_N^T P^T: wave w owns 128 output columns.
+//  * O^T = C_N^T P^T: wave w owns 128 output columns, read from LDS as
+//    16-byte runs: MFMA tile t (0..3) of half h takes as its row i the
+//    value dim 128w + 64h + 4i + t, so one ds_read_b128 of dims
+//    128w + 64h + 4i .. +3 feeds four MFMAs and the 16 lanes of a token row
+//    read 256 contiguous bytes. (Single floats at 16 consecutive dims, four
+//    token rows per instruction, put two rows on the same LDS banks.) The
+//    store undoes the permutation: lane (head j, g) of the four tiles holds
+//    the 16 dims of natural tile 8w + 4h + g.
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
 
@@ -30,6 +37,10 @@ constexpr int kRowChunks = kDK / 4;      // 16-byte chunks per row
 constexpr int kStage = kBT * kRowChunks / 256;
 constexpr int kKQ = kDK / 4;             // K per wave (144)
 constexpr int kPRow = kBT + 4;
+// partial S^T tiles [wave][token][head] with rows of 20 floats: the four
+// token rows a write or read instruction touches then start 16 banks apart
+// (rows of 16 put all four on the same 16 banks)
+constexpr int kSRow = kHT + 4;
 static_assert(kBT * kRowChunks % 256 == 0, "stage split");
 
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
@@ -43,7 +54,7 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                          int n_head_tiles, int xcd_remap, float scale_log2)
 {
     __shared__ __attribute__((aligned(16))) float s_c[2 * kBT * kRow];
-    __shared__ __attribute__((aligned(16))) float s_s[4 * kBT * kHT];
+    __shared__ __attribute__((aligned(16))) float s_s[4 * kBT * kSRow];
     __shared__ float s_p[kHT * kPRow];
 
     const int tid = threadIdx.x;
@@ -164,7 +175,7 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                s_s[(wave * kBT + 4 * g + i) * kHT + l16] = acc[i];
+                s_s[(wave * kBT + 4 * g + i) * kSRow + l16] = acc[i];
             __syncthreads();
 
             // ---- full tile, softmax (every wave, identical results)
@@ -172,8 +183,8 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
             float mx = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int r = (4 * g + i) * kHT + l16;
-                const float sdot = ((s_s[r] + s_s[kBT * kHT + r]) + s_s[2 * kBT * kHT + r]) + s_s[3 * kBT * kHT + r];
+                const int r = (4 * g + i) * kSRow + l16;
+                const float sdot = ((s_s[r] + s_s[kBT * kSRow + r]) + s_s[2 * kBT * kSRow + r]) + s_s[3 * kBT * kSRow + r];
                 sv[i] = (t0 + 4 * g + i) < p_hi ? sdot * scale_log2 : -INFINITY;
                 mx = fmaxf(mx, sv[i]);
             }
@@ -197,17 +208,22 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                 load_stage(t0 + 2 * kBT);
             __syncthreads();
 
-            // ---- O^T[dims 128*wave .. +128][heads] += C_N^T P^T
+            // ---- O^T[dims 128*wave .. +128][heads] += C_N^T P^T; o[4h + t]
+            // row i is dim 128*wave + 64h + 4i + t
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt)
                 o[dt] *= alpha;
 #pragma unroll
             for (int ks = 0; ks < kBT / 4; ++ks) {
                 const float pbv = s_p[l16 * kPRow + 4 * ks + g];
-                const float *crow = cs + (4 * ks + g) * kRow + 128 * wave + l16;
+                const float *crow = cs + (4 * ks + g) * kRow + 128 * wave + 4 * l16;
 #pragma unroll
-                for (int dt = 0; dt < 8; ++dt)
-                    o[dt] = mfma16x16x4f32(crow[16 * dt], pbv, o[dt]);
+                for (int h = 0; h < 2; ++h) {
+                    const floatx4 a = *(const floatx4 *)(crow + 64 * h);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        o[4 * h + t] = mfma16x16x4f32(a[t], pbv, o[4 * h + t]);
+                }
             }
         }
 
@@ -216,13 +232,21 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
             __builtin_nontemporal_store(m_run, m_part + (size_t)slot * num_heads + head0 + tid);
             __builtin_nontemporal_store(lsum, l_part + (size_t)slot * num_heads + head0 + tid);
         }
-        // tile by tile in MFMA accumulator order: 1 KB of contiguous memory
-        // per store; nontemporal, as the partials are read once, by the
-        // combine (see mla_splitkv_fp16.hip)
-        float *obase = o_part + (size_t)slot * num_heads * kDV + lane * 4;
+        // in the MFMA accumulator order of natural 16 x 16 tiles (frag_offset):
+        // lane (head j, g) holds, over o[4h .. 4h+3], dims 16g .. 16g+15 of
+        // tile 8*wave + 4h + g, element r of o[4h + t] being dim 4r + t of
+        // it; each store writes 4 runs of 256 contiguous bytes. Nontemporal,
+        // as the partials are read once, by the combine (see
+        // mla_splitkv_fp16.hip)
+        float *obase = o_part + (size_t)slot * num_heads * kDV;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            __builtin_nontemporal_store(o[dt], (floatx4 *)(obase + frag_offset(head0, 128 * wave + 16 * dt)));
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const floatx4 v = {o[4 * h][r], o[4 * h + 1][r], o[4 * h + 2][r], o[4 * h + 3][r]};
+                __builtin_nontemporal_store(
+                    v, (floatx4 *)(obase + frag_offset(head0 + l16, 128 * wave + 64 * h + 16 * g + 4 * r)));
+            }
     }
 }
 
