@@ -413,12 +413,18 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         if (T::kWaves > 8 && wave >= 8)
             return;
         const E *qb = q + ((size_t)b * num_heads + head0) * kDK;
+        // Q* rows past the tile's HT (16-head tiles: waves 4..7, and the rope
+        // units of waves 2, 3) are not loaded: nothing reads them, and as
+        // clamped re-reads of the last row they cost 18 of the prologue's
+        // 126 KB per CU. (The waits count younger loads only, so a wave that
+        // issues fewer Q* units waits the same way.)
 #pragma unroll
         for (int j = 0; j < T::kQBlocks; ++j) {
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                dma_row(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, 4 * wave + r);
-            if (wave < 4)
+                if (4 * wave + r < HT - 32 * j)
+                    dma_row(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, 4 * wave + r);
+            if (wave < 4 && 8 * wave < HT - 32 * j)
                 dma_rope(qb + (size_t)32 * j * kDK, HT - 1 - 32 * j, T::kPre + j, wave);
         }
         int pages[T::kPre];  // all page reads first: one wait for them all
