@@ -45,6 +45,8 @@ _SIGNATURES = {
     "mla_decode_fused_fp32": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "mla_decode_split_batched_workspace_size": (_sz, [_i, _i, _i, _i]),
     "mla_decode_split_batched_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+    "mla_decode_split_batched_fp16_partials": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+    "mla_decode_split_batched_fp16_combine": (_i, [_vp, _sz, _vp, _vp, _i, _i, _i, _i, _vp]),
     "mla_decode_split_bf16": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "mla_decode_split_batched_bf16": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "mla_decode_paged_workspace_size": (_sz, [_i, _i, _i, _i]),

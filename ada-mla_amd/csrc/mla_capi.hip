@@ -563,6 +563,29 @@ int mla_decode_split_batched_fp16(const void *query, const void *cache, const in
                            batch, num_heads, total_tokens, num_splits, 0u, stream);
 }
 
+int mla_decode_split_batched_fp16_partials(const void *query, const void *cache, const int *cu_seqlens,
+                                           void *workspace, size_t workspace_bytes, int batch, int num_heads,
+                                           int total_tokens, int num_splits, void *stream)
+{
+    if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0 || !cu_seqlens)
+        return MLA_STATUS_INVALID_VALUE;
+    if (total_tokens == 0 && !cache)
+        cache = query;  // nothing is read from the cache
+    return mla::run_decode(mla::Dtype::kF16, query, cache, cu_seqlens, nullptr, workspace, workspace_bytes,
+                           batch, num_heads, total_tokens, num_splits, 0u, stream, mla::kPhaseSplit);
+}
+
+int mla_decode_split_batched_fp16_combine(const void *workspace, size_t workspace_bytes, const int *cu_seqlens,
+                                          void *out, int batch, int num_heads, int total_tokens, int num_splits,
+                                          void *stream)
+{
+    if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0 || !cu_seqlens)
+        return MLA_STATUS_INVALID_VALUE;
+    return mla::run_decode(mla::Dtype::kF16, nullptr, nullptr, cu_seqlens, out, const_cast<void *>(workspace),
+                           workspace_bytes, batch, num_heads, total_tokens, num_splits, 0u, stream,
+                           mla::kPhaseCombine);
+}
+
 size_t mla_decode_paged_workspace_size(int batch, int num_heads, int total_tokens, int num_splits)
 {
     if (!mla::heads_ok(num_heads) || batch < 1 || total_tokens < 0)

@@ -20,16 +20,20 @@ by zeroing a 256 MB buffer before each timed call (mla.py:122-130).
 
 Timing is HIP events on the launch stream: one pair around all K calls
 (`value`, us/call), one pair around K back-to-back split-kernel launches
-(`roofline.kernel_us`, the dominant kernel alone). `roofline.frac` is over the
-whole call (algorithmic bytes / call time / 8 TB/s); `roofline.kernel_frac`
-over the split kernel alone.
+(`roofline.kernel_us`, the dominant kernel alone: single sequences and
+batches). `roofline.frac` is over the whole call (algorithmic bytes / call
+time / 8 TB/s); `roofline.kernel_frac` over the split kernel alone.
+`roofline.traffic` is the split kernel's HBM bytes per launch and
+`roofline.traffic_call` the whole call's (every kernel), both from the
+committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, with their ratios to the
+algorithmic bytes.
 
 Prints ONE JSON line. With the default workload the line also carries
 `other_configs`: BASELINE configs 3, 4 and 5 (N = 65536 with fp32 partials,
 n_h = 16, batched B = 32) measured the same way in the same run. --workload
 picks another configuration (n65536, nh16, batched, paged, block, bf16, the fp8
-cache workloads, fp32, fp32_n4096 and n256, a short sequence on the one-launch
-path) as the main line.
+cache workloads, fp32, fp32_n4096, n256, a short sequence on the one-launch
+path, and n32, the shortest call: the library's fixed cost) as the main line.
 """
 from __future__ import annotations
 
@@ -62,6 +66,8 @@ WORKLOADS = {
     "nh16": dict(kind="fp16", n_h=16, n=32768, desc="fp16 low-head, n_h=16, N=32768 (BASELINE config 4)"),
     "n256": dict(kind="fp16", n_h=128, n=256, desc="fp16 short sequence, n_h=128, N=256 (one split: the one-launch "
                                                   "path, no combine)"),
+    "n32": dict(kind="fp16", n_h=128, n=32, desc="fp16 shortest call, n_h=128, N=32 (one 32-token block, one launch, "
+                                                "no combine): the library's fixed cost per call"),
     "batched": dict(kind="batched", n_h=128, batch=32,
                     desc="fp16 batched, B=32, N_b ~ U[512,16384] seed 42 (BASELINE config 5)"),
     "fp32": dict(kind="fp32", n_h=128, n=1024, desc="fp32 path, n_h=128, N=1024 (BASELINE config 1 shape on GPU)"),
@@ -106,17 +112,20 @@ def roof_kernel_key(kind):
 
 
 def hbm_traffic(workload, kernel):
-    """HBM bytes per launch of the dominant kernel (FETCH_SIZE + WRITE_SIZE, each
-    scaled by its reading for a known-size device copy), from the committed
-    rocprofv3 --pmc summary profiles/hbm_traffic.json, or None when that file has
-    no entry for this workload."""
+    """HBM bytes per launch of the dominant kernel and per whole call (every
+    kernel of the call: FETCH_SIZE + WRITE_SIZE, each scaled by its reading for
+    a known-size device copy), from the committed rocprofv3 --pmc summary
+    profiles/hbm_traffic.json, or None when that file has no entry for this
+    workload."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         with open(path) as f:
-            entry = json.load(f)["workloads"][workload][kernel]
+            entries = json.load(f)["workloads"][workload]
+        entry = entries[kernel]
     except (OSError, KeyError, ValueError):
-        return None, None
-    return entry["fetch_bytes"] + entry["write_bytes"], "profiles/hbm_traffic_fetch_write.txt"
+        return None, None, None
+    call = sum(e["fetch_bytes"] + e["write_bytes"] for e in entries.values())
+    return entry["fetch_bytes"] + entry["write_bytes"], call, "profiles/hbm_traffic_fetch_write.txt"
 
 
 def cpu_info():
@@ -296,7 +305,13 @@ class Runner:
         return i
 
     def split_only(self):
-        """The split kernel alone (fp16 single sequence); the whole call otherwise."""
+        """The split kernel alone (fp16 single sequence or fp16 batch); the whole call otherwise."""
+        if self.kind == "batched":
+            i = self._next()
+            self._check(self.lib.mla_decode_split_batched_fp16_partials(
+                self.qs[i].data_ptr(), self.cs[i].data_ptr(), self.cu_d.data_ptr(), self.ws.data_ptr(), self.ws_bytes,
+                self.batch, self.n_h, self.total, self.splits, self.sptr), "batched partials")
+            return
         if self.kind != "fp16":
             return self.call()
         i = self._next()
@@ -386,9 +401,14 @@ def roofline(r, us_call, k_us):
     roof = {"bound": "hbm" if hbm else "mfma", "achieved": per_us / us_call, "peak": peak,
             "unit": "GB/s" if hbm else "TFLOP/s", "frac": per_us / us_call / peak,
             "frac_over": "whole call (every kernel of one decode call, back to back)"}
-    traffic, src = hbm_traffic(r.name, roof_kernel_key(r.kind))
+    traffic, traffic_call, src = hbm_traffic(r.name, roof_kernel_key(r.kind))
     roof.update({
         "traffic": traffic,
+        "traffic_of": "the split kernel alone (FETCH + WRITE, HBM side)",
+        "traffic_over_algorithmic": (traffic / alg_bytes) if traffic else None,
+        "traffic_call": traffic_call,
+        "traffic_call_of": "every kernel of the call (split partials written and read back included)",
+        "traffic_call_over_algorithmic": (traffic_call / alg_bytes) if traffic_call else None,
         "traffic_source": src,
         "kernel": ("splitkv_fp32_kernel + combine" if r.kind == "fp32" else
                    "absorb + splitkv_fp16_kernel + combine + projections" if r.kind == "block" else
@@ -412,7 +432,7 @@ def measure(torch, stream, r, steps, warmup, spinup_s):
         r.call()
     torch.cuda.synchronize()
     us_call = time_loop(torch, stream, r.call, steps)
-    k_us = time_loop(torch, stream, r.split_only, steps) if r.kind == "fp16" else None
+    k_us = time_loop(torch, stream, r.split_only, steps) if r.kind in ("fp16", "batched") else None
     return us_call, k_us
 
 
@@ -478,7 +498,7 @@ def main():
     r = Runner(lib, capi, torch, args.workload, dev, stream, args.flush_mb, args.partials, args.num_splits)
     us_call, k_us = measure(torch, stream, r, K, W, args.spinup_ms * 1e-3)
     roof, alg_bytes = roofline(r, us_call, k_us)
-    if r.kind in ("batched", "bf16", "paged", "block") + FP8_KINDS:
+    if r.kind in ("bf16", "paged", "block") + FP8_KINDS:
         roof["note"] = f"{r.kind} has no phase split: kernel_us is not measured separately"
 
     # the same K calls with the other partial precision (fresh buffers: the cursor runs on)

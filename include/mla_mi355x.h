@@ -194,6 +194,26 @@ int mla_decode_split_batched_fp16(const void *query, const void *cache,
                                   int batch, int num_heads, int total_tokens,
                                   int num_splits, void *stream);
 
+/* The two launches of mla_decode_split_batched_fp16, one at a time, as
+ * mla_decode_split_fp16_partials / _combine are for one sequence: the
+ * split-KV kernel leaves the partials in the workspace, the combine merges
+ * them into out. Called back to back on one stream with the same sizes they
+ * equal mla_decode_split_batched_fp16. No reference counterpart (the
+ * reference decodes one sequence per call). */
+int mla_decode_split_batched_fp16_partials(const void *query,
+                                           const void *cache,
+                                           const int *cu_seqlens,
+                                           void *workspace,
+                                           size_t workspace_bytes, int batch,
+                                           int num_heads, int total_tokens,
+                                           int num_splits, void *stream);
+int mla_decode_split_batched_fp16_combine(const void *workspace,
+                                          size_t workspace_bytes,
+                                          const int *cu_seqlens, void *out,
+                                          int batch, int num_heads,
+                                          int total_tokens, int num_splits,
+                                          void *stream);
+
 /* bf16 KV cache: mla_decode_split_fp16 and mla_decode_split_batched_fp16
  * with query, cache and out in bf16 (the same workspace sizes; bf16 MFMAs,
  * fp32 accumulation and softmax state, P and the normalised partials in

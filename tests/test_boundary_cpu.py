@@ -116,6 +116,20 @@ def test_batched_argument_errors(fn):
     assert f(FAKE, FAKE, FAKE, FAKE, FAKE, 16, 4, 128, 100, 0, None) == capi.STATUS_WORKSPACE_TOO_SMALL
 
 
+def test_batched_two_phase_argument_errors():
+    lib = capi.load()
+    p, c = lib.mla_decode_split_batched_fp16_partials, lib.mla_decode_split_batched_fp16_combine
+    # no cu_seqlens, no workspace, batch 0, a head count that is not a multiple of 16
+    assert p(FAKE, FAKE, None, FAKE, 1 << 30, 4, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
+    assert p(FAKE, FAKE, FAKE, None, 1 << 30, 4, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
+    assert p(FAKE, FAKE, FAKE, FAKE, 1 << 30, 0, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
+    assert p(FAKE, FAKE, FAKE, FAKE, 1 << 30, 4, 24, 100, 0, None) == capi.STATUS_INVALID_VALUE
+    assert p(FAKE, FAKE, FAKE, FAKE, 16, 4, 128, 100, 0, None) == capi.STATUS_WORKSPACE_TOO_SMALL
+    assert c(FAKE, 1 << 30, None, FAKE, 4, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
+    assert c(FAKE, 1 << 30, FAKE, None, 4, 128, 100, 0, None) == capi.STATUS_INVALID_VALUE
+    assert c(FAKE, 16, FAKE, FAKE, 4, 128, 100, 0, None) == capi.STATUS_WORKSPACE_TOO_SMALL
+
+
 # --------------------------------------------------------- torch extension
 
 def _ext():

@@ -491,3 +491,29 @@ def test_two_phase_api_equals_single_call(flags):
     assert lib.mla_decode_split_fp16_combine(ws.data_ptr(), ws_bytes, out.data_ptr(), 128, 3000, 0, flags, s) == 0
     torch.cuda.synchronize()
     assert torch.equal(one, out)
+
+
+@pytest.mark.parametrize("splits", [0, 7])
+def test_batched_two_phase_api_equals_single_call(splits):
+    # mla_decode_split_batched_fp16_partials then _combine are the batched
+    # call's two launches: bitwise equal output, empty sequences included
+    lib = capi.load()
+    seqlens = np.array([700, 0, 33, 4100, 1, 0, 2500])
+    q, c, cu = synthetic.batched_inputs(128, seqlens, seed=12)
+    qt, ct, cut = _t(q), _t(c), _t(cu)
+    B, n_h, total = len(seqlens), 128, int(seqlens.sum())
+    one = capi.decode_split_batched_fp16(qt, ct, cut, num_splits=splits)
+    out = torch.full_like(one, float("nan"))
+    ws_bytes = lib.mla_decode_split_batched_workspace_size(B, n_h, total, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qt.device)
+    s = capi._stream(qt)
+    assert lib.mla_decode_split_batched_fp16_partials(qt.data_ptr(), ct.data_ptr(), cut.data_ptr(), ws.data_ptr(),
+                                                      ws_bytes, B, n_h, total, splits, s) == 0
+    assert lib.mla_decode_split_batched_fp16_combine(ws.data_ptr(), ws_bytes, cut.data_ptr(), out.data_ptr(), B,
+                                                     n_h, total, splits, s) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(one, out)
+    ref = O.closed_form_batched(q, c, cu)
+    got = out.float().cpu().numpy()
+    for b in range(B):
+        np.testing.assert_allclose(got[b], ref[b], atol=1e-2, rtol=1e-2, err_msg=f"sequence {b}")
