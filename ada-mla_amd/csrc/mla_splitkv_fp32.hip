@@ -26,8 +26,31 @@
 //    the 16 dims of natural tile 8w + 4h + g.
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
+#include "mla_ring.hpp"
 
 namespace mla {
+
+#ifdef MLA_TIMELINE
+// Timeline build only (see mla_splitkv_fp16.hip): per workgroup of the fp32
+// kernel, wave 0 records s_memrealtime at entry, at the first block, at the
+// end of the block loop and after the partial store (stores complete), and
+// s_memtime sums over the blocks of its three phases: the first product (to
+// the barrier after the partial logits), the softmax and C staging (to the
+// next barrier) and the second product.
+constexpr int kTimelineWorkgroupsF32 = 8192;
+__device__ unsigned long long mla_timeline_stamps_f32[kTimelineWorkgroupsF32 * 16];
+#define MLA_STAMP32(e, v)                                                                  \
+    do {                                                                                   \
+        if (wave == 0 && lane == 0 && blockIdx.x < kTimelineWorkgroupsF32)                 \
+            mla_timeline_stamps_f32[blockIdx.x * 16 + (e)] = (unsigned long long)(v);      \
+    } while (0)
+#define MLA_MT32() __builtin_amdgcn_s_memtime()
+#else
+#define MLA_STAMP32(e, v) \
+    do {                  \
+    } while (0)
+#endif
+
 namespace {
 
 constexpr int kHT = 16;                  // heads per workgroup
@@ -62,6 +85,10 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
     const int wave = tid >> 6;
     const int l16 = lane & 15;
     const int g = lane >> 4;
+    MLA_STAMP32(0, __builtin_amdgcn_s_memrealtime());
+#ifdef MLA_TIMELINE
+    unsigned long long ph_s = 0, ph_x = 0, ph_o = 0, tm = 0;
+#endif
 
     int split, ht;
     {
@@ -155,8 +182,13 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
             o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
         __syncthreads();
+        MLA_STAMP32(1, __builtin_amdgcn_s_memrealtime());
+        MLA_STAMP32(11, nblk);
 
         for (int blk = 0; blk < nblk; ++blk) {
+#ifdef MLA_TIMELINE
+            tm = MLA_MT32();
+#endif
             const int cur = blk & 1;
             const int t0 = p_lo + blk * kBT;
             const float *cs = s_c + cur * kBT * kRow;
@@ -177,6 +209,9 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
             for (int i = 0; i < 4; ++i)
                 s_s[(wave * kBT + 4 * g + i) * kSRow + l16] = acc[i];
             __syncthreads();
+#ifdef MLA_TIMELINE
+            { const unsigned long long t2 = MLA_MT32(); ph_s += t2 - tm; tm = t2; }
+#endif
 
             // ---- full tile, softmax (every wave, identical results)
             float sv[4];
@@ -207,6 +242,9 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
             if (blk + 2 < nblk)
                 load_stage(t0 + 2 * kBT);
             __syncthreads();
+#ifdef MLA_TIMELINE
+            { const unsigned long long t2 = MLA_MT32(); ph_x += t2 - tm; tm = t2; }
+#endif
 
             // ---- O^T[dims 128*wave .. +128][heads] += C_N^T P^T; o[4h + t]
             // row i is dim 128*wave + 64h + 4i + t
@@ -225,7 +263,16 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                         o[4 * h + t] = mfma16x16x4f32(a[t], pbv, o[4 * h + t]);
                 }
             }
+#ifdef MLA_TIMELINE
+            { const unsigned long long t2 = MLA_MT32(); ph_o += t2 - tm; }
+#endif
         }
+        MLA_STAMP32(2, __builtin_amdgcn_s_memrealtime());
+#ifdef MLA_TIMELINE
+        MLA_STAMP32(6, ph_s);
+        MLA_STAMP32(7, ph_x);
+        MLA_STAMP32(8, ph_o);
+#endif
 
         const float lsum = sum_over_lane_groups(l_run);
         if (tid < kHT) {
@@ -247,6 +294,10 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                 __builtin_nontemporal_store(
                     v, (floatx4 *)(obase + frag_offset(head0 + l16, 128 * wave + 64 * h + 16 * g + 4 * r)));
             }
+#ifdef MLA_TIMELINE
+        MLA_WAIT_VMCNT(0);
+#endif
+        MLA_STAMP32(3, __builtin_amdgcn_s_memrealtime());
     }
 }
 
@@ -267,3 +318,11 @@ hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p, const Partials 
 }
 
 }  // namespace mla
+
+#ifdef MLA_TIMELINE
+extern "C" int mla_timeline_read_f32(void *dst, size_t bytes)
+{
+    const size_t n = bytes < sizeof(mla::mla_timeline_stamps_f32) ? bytes : sizeof(mla::mla_timeline_stamps_f32);
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(mla::mla_timeline_stamps_f32), n, 0, hipMemcpyDeviceToHost);
+}
+#endif

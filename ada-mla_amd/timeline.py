@@ -24,6 +24,13 @@ A sweep over the sequence length at a fixed split count (--sweep) gives the
 step cost with every CU busy as the slope of the launch time over blocks per
 workgroup, and the fixed cost per launch as its intercept.
 
+--fp32 reads the fp32 kernel's stamps instead (calls through
+mla_decode_fused_fp32, so launch_us includes the combine): entry, first
+block, loop end and partials stored, and per 16-token block the shader cycles
+of wave 0's three phases -- the first product (to the barrier after the
+partial logits), the softmax and C staging (to the next barrier) and the
+second product.
+
 Usage (single sequences, inputs rotated over >= 1 GB so that C comes from HBM):
   python ada-mla_amd/timeline.py --heads 128 --tokens 65536 --splits 128 --head-tile 64
   python ada-mla_amd/timeline.py --heads 128 --tokens 16384,32768,65536,131072 --splits 128 --head-tile 64 --sweep
@@ -115,6 +122,69 @@ def run_case(lib, torch, n_h, n, splits, flags, k, spin_s):
     return rec
 
 
+def run_case_f32(lib, torch, n_h, n, splits, k, spin_s):
+    vp = ctypes.c_void_p
+    import numpy as np
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = vp(stream.cuda_stream)
+    set_bytes = (n + n_h) * 576 * 4
+    pool = min(64, max(2, math.ceil(1024 * 2**20 / set_bytes) + 1))
+    qs = [torch.randn(n_h, 576, device=dev) for _ in range(pool)]
+    cs = [torch.randn(n, 576, device=dev) for _ in range(pool)]
+    out = torch.empty(n_h, 512, device=dev)
+    wsb = lib.mla_decode_fused_workspace_size(n_h, n, splits)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    cursor = [0]
+
+    def launch():
+        i = cursor[0] % pool
+        cursor[0] += 1
+        st = lib.mla_decode_fused_fp32(qs[i].data_ptr(), cs[i].data_ptr(), out.data_ptr(), ws.data_ptr(), wsb, n_h,
+                                       576, n, splits, sp)
+        if st != 0:
+            raise RuntimeError(f"mla_decode_fused_fp32: status {st}")
+
+    t_end = time.perf_counter() + spin_s
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            launch()
+        torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(k):
+        launch()
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000.0 / k
+    buf = np.zeros(8192 * SLOTS, dtype=np.uint64)
+    if lib.mla_timeline_read_f32(buf.ctypes.data, buf.nbytes) != 0:
+        raise RuntimeError("mla_timeline_read_f32 failed")
+    x = buf.reshape(8192, SLOTS).astype(np.int64)
+    x = x[(x[:, 3] > x[:, 0]) & (x[:, 0] > 0)]
+    x = x[x[:, 0] >= x[:, 0].max() - 100000]  # this launch's workgroups (within 1 ms of the last entry)
+    t0 = x[:, 0].min()
+    phases = {}
+    for name, e in (("entry", 0), ("first_block", 1), ("loop_end", 2), ("stored", 3)):
+        v = (x[:, e] - t0) * 0.01
+        phases[name] = [round(float(np.median(v)), 2), round(float(v.min()), 2), round(float(v.max()), 2)]
+    nblk = x[:, 11].astype(np.float64)
+    cyc = x[:, 6] + x[:, 7] + x[:, 8]
+    clk = float(np.median(cyc / ((x[:, 2] - x[:, 1]) * 0.01 * 1e3)))
+    rec = dict(path="fp32", heads=n_h, tokens=n, workgroups=int(len(x)), blocks=int(np.median(nblk)),
+               call_us=round(us, 2), span_us=round(float((x[:, 3].max() - t0) * 0.01), 2), clock_ghz=round(clk, 3),
+               block_cycles=round(float(np.median(cyc / nblk))),
+               first_product_cycles=round(float(np.median(x[:, 6] / nblk))),
+               softmax_staging_cycles=round(float(np.median(x[:, 7] / nblk))),
+               second_product_cycles=round(float(np.median(x[:, 8] / nblk))),
+               phases_med_min_max_us=phases)
+    del qs, cs, ws
+    torch.cuda.empty_cache()
+    return rec
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--heads", type=int, default=128)
@@ -125,6 +195,7 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="fit launch time = fixed + blocks x step")
     ap.add_argument("--calls", type=int, default=20)
     ap.add_argument("--spin-s", type=float, default=1.0)
+    ap.add_argument("--fp32", action="store_true", help="the fp32 kernel (mla_decode_fused_fp32)")
     args = ap.parse_args()
     if not os.path.exists(LIB):
         raise SystemExit(f"{LIB} is not built (python ada-mla_amd/build.py --timeline)")
@@ -139,6 +210,14 @@ def main():
     lib.mla_decode_split_head_tile.argtypes = [i_, i_, i_, u_]
     lib.mla_decode_split_num_splits.argtypes = [i_, i_, i_, u_]
     lib.mla_timeline_read.argtypes = [vp, sz]
+    lib.mla_timeline_read_f32.argtypes = [vp, sz]
+    lib.mla_decode_fused_workspace_size.restype = sz
+    lib.mla_decode_fused_workspace_size.argtypes = [i_, i_, i_]
+    lib.mla_decode_fused_fp32.argtypes = [vp, vp, vp, vp, sz, i_, i_, i_, i_, vp]
+    if args.fp32:
+        for n in (int(t) for t in args.tokens.split(",")):
+            print(json.dumps(run_case_f32(lib, torch, args.heads, n, args.splits, args.calls, args.spin_s)), flush=True)
+        return 0
     flags = FLAG_FP32_PARTIALS if args.partials == "fp32" else 0
     recs = []
     for n in (int(t) for t in args.tokens.split(",")):
