@@ -415,9 +415,9 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
         const E *qb = q + ((size_t)b * num_heads + head0) * kDK;
         // Q* rows past the tile's HT (16-head tiles: waves 4..7, and the rope
         // units of waves 2, 3) are not loaded: nothing reads them, and as
-        // clamped re-reads of the last row they cost 18 of the prologue's
-        // 126 KB per CU. (The waits count younger loads only, so a wave that
-        // issues fewer Q* units waits the same way.)
+        // clamped re-reads of the last row they cost 18 KB of the 144 KB
+        // the prologue issued per CU. (The waits count younger loads only, so
+        // a wave that issues fewer Q* units waits the same way.)
 #pragma unroll
         for (int j = 0; j < T::kQBlocks; ++j) {
 #pragma unroll
