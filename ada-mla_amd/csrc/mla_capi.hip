@@ -309,9 +309,13 @@ int choose_merge(const Plan &p, bool single16, unsigned flags)
 // stored partials faster. Same box, plain against nontemporal: n_h = 16
 // (32 combine workgroups) 15.55 -> 14.80 us; N = 4096 (256) 10.77 -> 11.01 us,
 // N = 65536 with fp32 partials (256) 37.4 -> 38.3 us, batched (512) 94.2 -> 93.5.
+// The quarter-tile combine (fewer (tile, sequence) items than CUs) also
+// reads plain stored partials faster: n_h = 16, 128 splits (128 combine
+// workgroups of 8 waves) 14.07 -> 13.82 us.
 int choose_part_plain(const Plan &p, int batch, int num_heads, int cu_count)
 {
-    return 4 * combine_workgroups(p, batch, num_heads) < cu_count ? 1 : 0;
+    const int items = num_heads / 16 * (kDV / 16) * batch;
+    return (items < cu_count || 4 * combine_workgroups(p, batch, num_heads, cu_count) < cu_count) ? 1 : 0;
 }
 
 // Shared body of every entry point; `phases` selects the split kernel, the

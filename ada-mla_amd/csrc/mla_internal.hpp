@@ -116,7 +116,7 @@ hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p,
 // The output has the partials' type: fp16 / bf16 on the 16-bit path, fp32
 // on the fp32 path.
 // Workgroups of the combine launch for plan p (batch sequences, num_heads).
-int combine_workgroups(const Plan &p, int batch, int num_heads);
+int combine_workgroups(const Plan &p, int batch, int num_heads, int cu_count);
 
 hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
                           hipStream_t s);

@@ -24,6 +24,12 @@ A sweep over the sequence length at a fixed split count (--sweep) gives the
 step cost with every CU busy as the slope of the launch time over blocks per
 workgroup, and the fixed cost per launch as its intercept.
 
+--combine times whole calls (split kernel, then combine) and reads, besides the
+split kernel's stamps, the combine's per-wave stamps of the last call: entry,
+slots merged (every load landed), before the store, store complete; gap_us is
+the time from the split kernel's last partial store to the first combine
+wave's entry.
+
 --fp32 reads the fp32 kernel's stamps instead (calls through
 mla_decode_fused_fp32, so launch_us includes the combine): entry, first
 block, loop end and partials stored, and per 16-token block the shader cycles
@@ -122,6 +128,87 @@ def run_case(lib, torch, n_h, n, splits, flags, k, spin_s):
     return rec
 
 
+def run_case_combine(lib, torch, n_h, n, splits, flags, k, spin_s):
+    """Whole calls (split kernel, then combine_kernel): the split kernel's
+    stamps and the combine's per-wave stamps of the last call, both relative
+    to the split kernel's first workgroup entry."""
+    import numpy as np
+    vp = ctypes.c_void_p
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = vp(stream.cuda_stream)
+    set_bytes = n * 576 * 2 + n_h * 576 * 2
+    pool = min(64, max(2, math.ceil(1024 * 2**20 / set_bytes) + 1))
+    qs = [torch.randn(n_h, 576, device=dev, dtype=torch.float16) for _ in range(pool)]
+    cs = [torch.randn(n, 576, device=dev, dtype=torch.float16) for _ in range(pool)]
+    out = torch.empty(n_h, 512, device=dev, dtype=torch.float16)
+    wsb = lib.mla_decode_split_workspace_size(n_h, n, splits)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    ht = lib.mla_decode_split_head_tile(n_h, n, splits, flags)
+    ns = lib.mla_decode_split_num_splits(n_h, n, splits, flags)
+    if lib.mla_decode_split_launches(n_h, n, splits, flags) != 2:
+        raise SystemExit("this plan makes one launch (no combine)")
+    n_wg = ((ns + 7) // 8 * 8) * (n_h // ht)
+    cursor = [0]
+
+    def launch():
+        i = cursor[0] % pool
+        cursor[0] += 1
+        st = lib.mla_decode_split_fp16_ex(qs[i].data_ptr(), cs[i].data_ptr(), out.data_ptr(), ws.data_ptr(), wsb,
+                                          n_h, n, splits, flags, sp)
+        if st != 0:
+            raise RuntimeError(f"mla_decode_split_fp16_ex: status {st}")
+
+    t_end = time.perf_counter() + spin_s
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            launch()
+        torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(k):
+        launch()
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000.0 / k
+    if lib.mla_timeline_clear_combine() != 0:
+        raise RuntimeError("mla_timeline_clear_combine failed")
+    launch()  # the call whose stamps are read, after back-to-back ones
+    launch()
+    torch.cuda.synchronize()
+    buf = np.zeros(n_wg * SLOTS, dtype=np.uint64)
+    if lib.mla_timeline_read(buf.ctypes.data, buf.nbytes) != 0:
+        raise RuntimeError("mla_timeline_read failed")
+    x = buf.reshape(n_wg, SLOTS).astype(np.int64)
+    x = x[x[:, 10] > x[:, 0]]
+    cb = np.zeros(16384 * 4, dtype=np.uint64)
+    if lib.mla_timeline_read_combine(cb.ctypes.data, cb.nbytes) != 0:
+        raise RuntimeError("mla_timeline_read_combine failed")
+    c = cb.reshape(-1, 4).astype(np.int64)
+    c = c[c[:, 0] > 0]
+    t0 = x[:, 0].min()
+    split_end = max(x[:, 10].max(), x[:, 5].max())
+
+    def mmm(v):
+        v = (v - t0) * 0.01
+        return [round(float(np.median(v)), 2), round(float(v.min()), 2), round(float(v.max()), 2)]
+
+    rec = dict(heads=n_h, tokens=n, head_tile=int(ht), splits=int(ns),
+               partials="fp32" if flags & FLAG_FP32_PARTIALS else "fp16", call_us=round(us, 2),
+               split_workgroups=int(len(x)), combine_waves=int(len(c)),
+               split_entry=mmm(x[:, 0]), split_stored=mmm(np.maximum(x[:, 10], x[:, 5])),
+               split_end=round(float((split_end - t0) * 0.01), 2),
+               combine_entry=mmm(c[:, 0]), combine_merged=mmm(c[:, 1]), combine_before_store=mmm(c[:, 2]),
+               combine_stored=mmm(c[:, 3]),
+               gap_us=round(float((c[:, 0].min() - split_end) * 0.01), 2),
+               combine_span_us=round(float((c[:, 3].max() - c[:, 0].min()) * 0.01), 2))
+    del qs, cs, ws
+    torch.cuda.empty_cache()
+    return rec
+
+
 def run_case_f32(lib, torch, n_h, n, splits, k, spin_s):
     vp = ctypes.c_void_p
     import numpy as np
@@ -196,6 +283,8 @@ def main():
     ap.add_argument("--calls", type=int, default=20)
     ap.add_argument("--spin-s", type=float, default=1.0)
     ap.add_argument("--fp32", action="store_true", help="the fp32 kernel (mla_decode_fused_fp32)")
+    ap.add_argument("--combine", action="store_true",
+                    help="whole calls: the split kernel's end and the combine's per-wave stamps")
     args = ap.parse_args()
     if not os.path.exists(LIB):
         raise SystemExit(f"{LIB} is not built (python ada-mla_amd/build.py --timeline)")
@@ -214,11 +303,19 @@ def main():
     lib.mla_decode_fused_workspace_size.restype = sz
     lib.mla_decode_fused_workspace_size.argtypes = [i_, i_, i_]
     lib.mla_decode_fused_fp32.argtypes = [vp, vp, vp, vp, sz, i_, i_, i_, i_, vp]
+    lib.mla_decode_split_fp16_ex.argtypes = [vp, vp, vp, vp, sz, i_, i_, i_, u_, vp]
+    lib.mla_decode_split_launches.argtypes = [i_, i_, i_, u_]
+    lib.mla_timeline_read_combine.argtypes = [vp, sz]
     if args.fp32:
         for n in (int(t) for t in args.tokens.split(",")):
             print(json.dumps(run_case_f32(lib, torch, args.heads, n, args.splits, args.calls, args.spin_s)), flush=True)
         return 0
     flags = FLAG_FP32_PARTIALS if args.partials == "fp32" else 0
+    if args.combine:
+        for n in (int(t) for t in args.tokens.split(",")):
+            print(json.dumps(run_case_combine(lib, torch, args.heads, n, args.splits, flags, args.calls,
+                                              args.spin_s)), flush=True)
+        return 0
     recs = []
     for n in (int(t) for t in args.tokens.split(",")):
         rec = run_case(lib, torch, args.heads, n, args.splits, flags, args.calls, args.spin_s)

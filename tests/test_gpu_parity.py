@@ -475,6 +475,43 @@ def test_config3_n65536_fp32_partials():
     _check16(_fp16(q, c, flags=capi.FLAG_FP32_PARTIALS), O.closed_form(q, c), "config 3, fp32 partials")
 
 
+# ------------------------------------------ quarter-tile combine (few items)
+# With fewer (16 x 16 tile, sequence) items than CUs the combine merges
+# quarter tiles (16 heads x 4 dims): lane (j, h) takes slots 4 i + j, so a slot
+# count that is not a multiple of 4 leaves lanes without a slot, and more
+# than 16 waves x 16 slots take a second load batch per wave.
+
+@pytest.mark.parametrize("n_h,n,splits,flags", [
+    (16, 32768, 600, 0), (16, 32768, 600, 4), (16, 5000, 3, 0), (16, 70, 2, 0),
+    (32, 5000, 0, 0), (48, 1000, 77, 0), (64, 4096, 6, 4), (64, 20000, 0, 0)])
+def test_quarter_combine(n_h, n, splits, flags):
+    print(f"quarter combine n_h={n_h} N={n} splits={splits} flags={flags}", flush=True)
+    q, c = synthetic.decode_inputs(n_h, n, seed=700 + n_h + splits)
+    _check16(_fp16(q, c, num_splits=splits, flags=flags), O.closed_form(q, c),
+             f"n_h={n_h} N={n} splits={splits} flags={flags}")
+
+
+@pytest.mark.parametrize("n_h,n,splits", [(16, 3000, 0), (16, 3000, 300), (32, 777, 5)])
+def test_quarter_combine_fp32(n_h, n, splits):
+    print(f"quarter combine fp32 n_h={n_h} N={n} splits={splits}", flush=True)
+    q, c = synthetic.decode_inputs(n_h, n, seed=800 + n, dtype=np.float32)
+    _check32(_fp32(q, c, num_splits=splits), O.closed_form(q, c), f"n_h={n_h} N={n} splits={splits}")
+
+
+@pytest.mark.parametrize("splits", [0, 3, 50, 400])
+def test_quarter_combine_batched_ragged_with_empty(splits):
+    print(f"quarter combine batched splits={splits}", flush=True)
+    seqlens = np.array([5, 0, 17, 1000, 300, 64, 0])  # 7 x 32 tiles at 16 heads: 224 items
+    q, c, cu = synthetic.batched_inputs(16, seqlens, seed=19)
+    got = _batched(q, c, cu, num_splits=splits)
+    ref = O.closed_form_batched(q, c, cu)
+    for b in range(len(seqlens)):
+        if seqlens[b] == 0:
+            assert not got[b].any(), f"empty seq {b}"
+        else:
+            _check16(got[b], ref[b], f"seq {b} splits={splits}")
+
+
 @pytest.mark.parametrize("flags", [0, 4])
 def test_two_phase_api_equals_single_call(flags):
     # the two phases are the two-launch call's launches
