@@ -52,7 +52,14 @@ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // split reads). Measured at 128 heads, N = 1024: 16.7 us per call with
 // 32-token splits (256 workgroups), 18.4 us with 64-token splits (128).
 constexpr int kMinSplitTokensF32 = 32;
-constexpr int kTwoPerCuTokensF32 = 256;
+
+// fp32 path: 32-head workgroups once their chunks hold this many tokens (12
+// blocks). Measured per call on one box (16 / 32 heads per workgroup, the
+// planner's split counts): n_h = 128, N = 4096 24.5 / 29.9 us, N = 8192
+// 36.0 / 38.1, N = 12288 45.6 / 45.4 (192-token chunks at 32 heads),
+// N = 16384 57.3 / 55.4; n_h = 64, N = 8192 23.9 / 27.6, N = 32768 57.4 /
+// 55.4; n_h = 32, N = 16384 22.3 / 26.0.
+constexpr int kHt32MinChunkTokensF32 = 192;
 
 constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
@@ -163,20 +170,23 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch, bool se
         return p;
     }
     if (fp32) {
-        p.head_tile = 16;
         p.block_tokens = 16;
+        // one workgroup per CU (the kernel's LDS holds one) unless the split
+        // count is given
+        auto splits_for = [&](int ht) {
+            if (num_splits > 0)
+                return num_splits;
+            const int per_round = std::max(1, cu_count / (num_heads / ht));
+            return std::min(per_round, ceil_div(total_tokens, kMinSplitTokensF32));
+        };
+        // 32 heads per workgroup fill each C block once for twice the heads,
+        // but take twice the chunks' partials and half the chunks: they pay
+        // where their chunks hold at least kHt32MinChunkTokensF32 tokens.
+        p.head_tile = 16;
+        if (num_heads % 32 == 0 && ceil_div(total_tokens, splits_for(32)) >= kHt32MinChunkTokensF32)
+            p.head_tile = 32;
         p.n_head_tiles = num_heads / p.head_tile;
-        int w = num_splits;
-        if (w <= 0) {
-            // one workgroup per CU; two (the kernel's LDS and registers allow
-            // it) once each chunk still holds kTwoPerCuTokensF32 tokens.
-            // Measured at 128 heads: N = 16384 79.7 -> 66.6 us with two, while
-            // at N = 4096 (64-token chunks) two were slower (29.2 -> 30.8 us)
-            const int per_round = std::max(1, cu_count / p.n_head_tiles);
-            w = std::min(per_round, ceil_div(total_tokens, kMinSplitTokensF32));
-            if (total_tokens >= 2 * per_round * kTwoPerCuTokensF32)
-                w = 2 * per_round;
-        }
+        const int w = splits_for(p.head_tile);
         set_chunks(p, total_tokens, batch, w);
         p.part_bytes = 4;
         return p;

@@ -9,21 +9,35 @@
 // split so the grid fills the GPU, and the splits are merged by
 // mla_combine.hip.
 //
-// Workgroup = 4 wave64s, 16 heads, blocks of 16 tokens:
-//  * S^T = C Q*^T: wave w owns K-quarter [144w, 144w + 144) of the 16x16 tile
-//    (its Q* slice stays in VGPRs); the four partial tiles are summed through
-//    LDS. Each lane reads 4 consecutive K of both operands with one 16-byte
-//    LDS read and feeds them to 4 MFMAs (the same K permutation on A and B).
-//  * every wave then redoes the (tiny) softmax of the 16x16 tile, so all of
-//    them hold the running max and sum; wave 0 publishes P.
-//  * O^T = C_N^T P^T: wave w owns 128 output columns, read from LDS as
-//    16-byte runs: MFMA tile t (0..3) of half h takes as its row i the
-//    value dim 128w + 64h + 4i + t, so one ds_read_b128 of dims
+// Workgroup = 8 wave64s (two per SIMD), 16 heads, blocks of 16 tokens, in
+// two roles pipelined one block apart: at step t the S waves form the logits
+// and the softmax of block t while the O waves add block t - 1 into O, so
+// one wave's softmax and LDS traffic overlap the other's MFMAs on each SIMD.
+//  * S waves 0..3: S^T = C Q*^T, wave w owning K-quarter [144w, 144w + 144)
+//    of the 16x16 tile (its Q* slice stays in VGPRs); the four partial tiles
+//    are summed through LDS (barrier X), and every S wave redoes the (tiny)
+//    softmax, so all of them hold the running max and sum; wave 0 publishes P
+//    and the rescale factor of each head for the O waves. Each lane reads 4
+//    consecutive K of both operands with one 16-byte LDS read and feeds them
+//    to 4 MFMAs (the same K permutation on A and B).
+//  * O waves 4..7: O^T = C_N^T P^T, wave 4 + w owning 128 output columns,
+//    read from LDS as 16-byte runs: MFMA tile t (0..3) of half h takes as its
+//    row i the value dim 128w + 64h + 4i + t, so one ds_read_b128 of dims
 //    128w + 64h + 4i .. +3 feeds four MFMAs and the 16 lanes of a token row
-//    read 256 contiguous bytes. (Single floats at 16 consecutive dims, four
-//    token rows per instruction, put two rows on the same LDS banks.) The
-//    store undoes the permutation: lane (head j, g) of the four tiles holds
-//    the 16 dims of natural tile 8w + 4h + g.
+//    read 256 contiguous bytes. The store undoes the permutation: lane
+//    (head j, g) of the four tiles holds the 16 dims of natural tile
+//    8w + 4h + g. An O wave runs one of its block's four token quads before
+//    barrier X and three after, so that its MFMAs fill the S wave's softmax
+//    on the same SIMD.
+//  * C blocks go HBM -> LDS by the direct global->LDS load (36 loads of 1 KB
+//    per block: 20 issued by the O waves before their MFMAs, 16 by the S
+//    waves after their softmax) into a 4-slot ring, two blocks ahead of the
+//    S waves; rows are 2304 bytes with 16-byte chunk c of row r
+//    at c ^ (r mod 16), so the S waves' row reads (16 rows, one chunk) and
+//    the O waves' token-row reads (16 chunks of one row) both touch 16
+//    distinct chunk positions of a 256-byte bank period.
+#include <type_traits>
+
 #include "mla_device.hpp"
 #include "mla_internal.hpp"
 #include "mla_ring.hpp"
@@ -39,34 +53,53 @@ namespace mla {
 // next barrier) and the second product.
 constexpr int kTimelineWorkgroupsF32 = 8192;
 __device__ unsigned long long mla_timeline_stamps_f32[kTimelineWorkgroupsF32 * 16];
-#define MLA_STAMP32(e, v)                                                                  \
+#define MLA_STAMP32W(w, e, v)                                                              \
     do {                                                                                   \
-        if (wave == 0 && lane == 0 && blockIdx.x < kTimelineWorkgroupsF32)                 \
+        if (wave == (w) && lane == 0 && blockIdx.x < kTimelineWorkgroupsF32)               \
             mla_timeline_stamps_f32[blockIdx.x * 16 + (e)] = (unsigned long long)(v);      \
     } while (0)
+#define MLA_STAMP32(e, v) MLA_STAMP32W(0, e, v)
 #define MLA_MT32() __builtin_amdgcn_s_memtime()
 #else
 #define MLA_STAMP32(e, v) \
     do {                  \
     } while (0)
+#define MLA_STAMP32W(w, e, v) \
+    do {                      \
+    } while (0)
 #endif
 
 namespace {
 
-constexpr int kHT = 16;                  // heads per workgroup
 constexpr int kBT = 16;                  // tokens per block
-constexpr int kRow = kDK + 4;            // LDS row stride (floats): 2320 B
-constexpr int kRowChunks = kDK / 4;      // 16-byte chunks per row
-constexpr int kStage = kBT * kRowChunks / 256;
-constexpr int kKQ = kDK / 4;             // K per wave (144)
+constexpr int kRing = 4;                 // C ring slots
+constexpr int kRowChunks = kDK / 4;      // 16-byte chunks per row (144)
+constexpr int kSlot = kBT * kDK;         // floats per ring slot (36 KB)
+constexpr int kLoads = kSlot * 4 / 1024; // 1 KB direct loads per block (36)
+// O wave 4 + w issues units w, w + 4, ... (kLoadsO of them) before its first
+// MFMAs of a step, S wave w units 4 kLoadsO + w, + 4, ... (kLoadsS) after its
+// softmax: such a load holds its wave until it is accepted, so each role
+// issues its share where it has slack
+constexpr int kLoadsO = 5;
+constexpr int kLoadsS = 4;
+static_assert(4 * (kLoadsO + kLoadsS) == kLoads, "load split");
+constexpr int kWaves = 8;
+constexpr int kKQ = kDK / 4;             // K per S wave (144)
 constexpr int kPRow = kBT + 4;
-// partial S^T tiles [wave][token][head] with rows of 20 floats: the four
-// token rows a write or read instruction touches then start 16 banks apart
-// (rows of 16 put all four on the same 16 banks)
-constexpr int kSRow = kHT + 4;
-static_assert(kBT * kRowChunks % 256 == 0, "stage split");
+// partial S^T tiles [wave][head][token] with rows of 20 floats: lane
+// (head j, g) writes and reads tokens 4g .. 4g + 3 of row j as one 16-byte
+// access, and the 16 rows of an instruction then fall on 16 distinct 4-bank
+// groups
+constexpr int kSRow = kBT + 4;
+static_assert(kRowChunks % 16 == 0, "the row swizzle stays within a row");
+static_assert(kLoads == 36, "block loads");
 
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
+// HT: heads per workgroup (16 or 32), as HT / 16 sub-tiles of 16 heads that
+// every wave carries side by side: the S waves' C rows and the O waves' C_N
+// columns are read from LDS once for all of them, so a 32-head workgroup
+// fills each C block once for twice the heads.
+template <int HT>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kWaves, 64 * kWaves), amdgpu_waves_per_eu(2, 2)))
 void splitkv_fp32_kernel(const float *__restrict__ q,
                          const float *__restrict__ c,
                          const int *__restrict__ cu_seqlens,
@@ -76,18 +109,28 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                          int num_heads, int batch, int total_tokens, int chunk,
                          int n_head_tiles, int xcd_remap, float scale_log2)
 {
-    __shared__ __attribute__((aligned(16))) float s_c[2 * kBT * kRow];
-    __shared__ __attribute__((aligned(16))) float s_s[4 * kBT * kSRow];
-    __shared__ float s_p[kHT * kPRow];
+    constexpr int kNS = HT / 16;          // 16-head sub-tiles
+    // O waves' token quads before barrier X (the rest after it, beside the
+    // S waves' softmax)
+    constexpr int kQuadsA = kNS == 1 ? 1 : 2;
+    __shared__ __attribute__((aligned(1024))) float s_c[kRing * kSlot];
+    __shared__ __attribute__((aligned(16))) float s_s[4 * HT * kSRow];
+    __shared__ __attribute__((aligned(16))) float s_p[2 * HT * kPRow];
+    __shared__ float s_alpha[2 * HT];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool s_role = wave < 4;
+    const int w4 = wave & 3;  // K quarter (S waves) or 128-column group (O waves)
+    // S waves: the sub-tile whose softmax this wave runs (S waves w4 < kNS
+    // publish its P and rescale factors and store its m and l)
+    const int my_sh = w4 % kNS;
     const int l16 = lane & 15;
     const int g = lane >> 4;
     MLA_STAMP32(0, __builtin_amdgcn_s_memrealtime());
 #ifdef MLA_TIMELINE
-    unsigned long long ph_s = 0, ph_x = 0, ph_o = 0, tm = 0;
+    unsigned long long ph_a = 0, ph_b = 0, ph_o = 0, tm = 0, wk_a = 0, wk_b = 0;
 #endif
 
     int split, ht;
@@ -106,7 +149,7 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
         return;
     const int lo = split * chunk;
     const int hi = min(lo + chunk, total_tokens);
-    const int head0 = ht * kHT;
+    const int head0 = ht * HT;
 
     int b = 0;
     const int nseq = cu_seqlens ? batch : 1;
@@ -118,6 +161,9 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
         }
         b = l;
     }
+
+    // LDS float offset of (row, logical 16-byte chunk) in a slot
+    auto slot_at = [](int row, int ch) { return row * kDK + 4 * (ch ^ (row & 15)); };
 
     for (; b < nseq; ++b) {
         int seq_lo = 0, seq_hi = total_tokens;
@@ -134,166 +180,244 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
         const int slot = split + b;
         const int nblk = (p_hi - p_lo + kBT - 1) / kBT;
 
+        // the ring and the P / alpha buffers of a previous piece are free
         __syncthreads();
 
-        // Q* slice: head head0 + l16, dims kKQ*wave + 16*kq + 4*g .. +3
-        floatx4 qf[kKQ / 16];
-        {
-            const float *qrow = q + ((size_t)b * num_heads + head0 + l16) * kDK + kKQ * wave + 4 * g;
+        // block j's direct loads of this wave into ring slot j % kRing: unit
+        // u covers the slot's physical chunks [64u, 64u + 64); lane i's chunk
+        // p = 64u + i is row p / 144, stored chunk p % 144, i.e. logical
+        // chunk (p % 144) ^ (row mod 16). Rows past the piece repeat its last
+        // token (their logits are masked).
+        auto issue_block = [&](int j) {
+            const int t0 = p_lo + j * kBT;
+            const float *base = c + (size_t)t0 * kDK;
+            const float *dst = s_c + (j % kRing) * kSlot;
+            const int last = p_hi - 1 - t0;
 #pragma unroll
-            for (int kq = 0; kq < kKQ / 16; ++kq)
-                qf[kq] = *(const floatx4 *)(qrow + 16 * kq);
-        }
+            for (int k = 0; k < (s_role ? kLoadsS : kLoadsO); ++k) {
+                const int u = (s_role ? 4 * kLoadsO : 0) + w4 + 4 * k;
+                const int pch = 64 * u + lane;
+                const int row = pch / kRowChunks;
+                const int sch = pch - row * kRowChunks;
+                const int lch = sch ^ (row & 15);
+                const int src_row = min(row, last);
+                global_to_lds16(base, (src_row * kRowChunks + lch) * 16, dst + 256 * u);
+            }
+        };
 
-        floatx4 stage[kStage];
-        auto load_stage = [&](int t0) {
+        // The two roles run separate loops with the same barriers (two per
+        // step), so that the S waves' Q* and the O waves' accumulators share
+        // registers.
+        if (s_role) {
+            // Q* slices, head head0 + 16 sh + l16, dims kKQ*w4 + 16*kq + 4*g .. +3
+            floatx4 qf[kNS][kKQ / 16];
 #pragma unroll
-            for (int s = 0; s < kStage; ++s) {
-                const int ci = tid + 256 * s;
-                const int tok = ci / kRowChunks;
-                const int col = ci - tok * kRowChunks;
-                const int gt = t0 + tok;
-                if (gt < p_hi)
-                    stage[s] = *(const floatx4 *)(c + (size_t)gt * kDK + col * 4);
+            for (int sh = 0; sh < kNS; ++sh) {
+                const float *qrow = q + ((size_t)b * num_heads + head0 + 16 * sh + l16) * kDK + kKQ * w4 + 4 * g;
+#pragma unroll
+                for (int kq = 0; kq < kKQ / 16; ++kq)
+                    qf[sh][kq] = *(const floatx4 *)(qrow + 16 * kq);
+            }
+            issue_block(0);
+            if (nblk > 1)
+                issue_block(1);
+            // Q* in registers, blocks 0 and 1 landed. The wait is for every
+            // load: the compiler counts only its own loads (Q*), not the
+            // direct loads issued after them, so after a partial wait it would
+            // still take Q* as in flight and wait for it inside the block
+            // loop, where its vmcnt waits would then drain the ring loads of
+            // block t + 2 at every step.
+            MLA_WAIT_VMCNT(0);
+            __syncthreads();
+            MLA_STAMP32(1, __builtin_amdgcn_s_memrealtime());
+            MLA_STAMP32(11, nblk);
+
+            float m_run = -INFINITY, l_run = 0.f;  // sub-tile my_sh
+            for (int t = 0; t <= nblk; ++t) {
+#ifdef MLA_TIMELINE
+                tm = MLA_MT32();
+#endif
+                if (t < nblk) {
+                    // ---- partial S^T of block t over this wave's K-quarter
+                    const float *cs = s_c + (t % kRing) * kSlot;
+                    floatx4 acc[kNS];
+#pragma unroll
+                    for (int sh = 0; sh < kNS; ++sh)
+                        acc[sh] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kq = 0; kq < kKQ / 16; ++kq) {
+                        const floatx4 a = *(const floatx4 *)(cs + slot_at(l16, 36 * w4 + 4 * kq + g));
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                            for (int sh = 0; sh < kNS; ++sh)
+                                acc[sh] = mfma16x16x4f32(a[jj], qf[sh][kq][jj], acc[sh]);
+                    }
+#pragma unroll
+                    for (int sh = 0; sh < kNS; ++sh)
+                        *(floatx4 *)(s_s + (w4 * HT + 16 * sh + l16) * kSRow + 4 * g) = acc[sh];
+                }
+#ifdef MLA_TIMELINE
+                wk_a += MLA_MT32() - tm;
+#endif
+                __syncthreads();  // barrier X: the four partial S^T tiles are in LDS
+#ifdef MLA_TIMELINE
+                { const unsigned long long t2 = MLA_MT32(); ph_a += t2 - tm; tm = t2; }
+#endif
+                if (t < nblk) {
+                    // ---- full tile and softmax of sub-tile my_sh (every S
+                    // wave of the sub-tile, identical results)
+                    const int t0 = p_lo + t * kBT;
+                    const float *sp = s_s + (16 * my_sh + l16) * kSRow + 4 * g;
+                    const floatx4 sdot = ((*(const floatx4 *)sp + *(const floatx4 *)(sp + HT * kSRow)) +
+                                          *(const floatx4 *)(sp + 2 * HT * kSRow)) +
+                                         *(const floatx4 *)(sp + 3 * HT * kSRow);
+                    float sv[4];
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        sv[i] = (t0 + 4 * g + i) < p_hi ? sdot[i] * scale_log2 : -INFINITY;
+                        mx = fmaxf(mx, sv[i]);
+                    }
+                    mx = max_over_lane_groups(mx);
+                    const float mn = fmaxf(m_run, mx);
+                    const float alpha = fast_exp2(m_run - mn);
+                    m_run = mn;
+                    floatx4 pv;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        pv[i] = fast_exp2(sv[i] - mn);
+                    l_run = l_run * alpha + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+                    if (w4 < kNS) {
+                        *(floatx4 *)(s_p + (t & 1) * HT * kPRow + (16 * my_sh + l16) * kPRow + 4 * g) = pv;
+                        if (g == 0)
+                            s_alpha[(t & 1) * HT + 16 * my_sh + l16] = alpha;
+                    }
+                }
+                // the S waves' share of block t + 2; block t + 1 landed before
+                // the barrier (block t + 2's loads stay in flight)
+                if (t + 2 < nblk) {
+                    issue_block(t + 2);
+                    MLA_WAIT_VMCNT(kLoadsS);
+                } else {
+                    MLA_WAIT_VMCNT(0);
+                }
+#ifdef MLA_TIMELINE
+                { const unsigned long long t2 = MLA_MT32(); ph_b += t2 - tm; wk_b += t2 - tm; tm = t2; }
+#endif
+                __syncthreads();  // barrier Y: P and alpha of block t, block t + 1 are in LDS
+#ifdef MLA_TIMELINE
+                { const unsigned long long t2 = MLA_MT32(); ph_o += t2 - tm; }
+#endif
+            }
+            MLA_STAMP32(2, __builtin_amdgcn_s_memrealtime());
+#ifdef MLA_TIMELINE
+            MLA_STAMP32(6, ph_a);
+            MLA_STAMP32(7, ph_b);
+            MLA_STAMP32(8, ph_o);
+            MLA_STAMP32W(0, 4, wk_a);
+            MLA_STAMP32W(0, 5, wk_b);
+#endif
+            const float lsum = sum_over_lane_groups(l_run);
+            if (w4 < kNS && lane < 16) {
+                const size_t mi = (size_t)slot * num_heads + head0 + 16 * my_sh + lane;
+                __builtin_nontemporal_store(m_run, m_part + mi);
+                __builtin_nontemporal_store(lsum, l_part + mi);
+            }
+        } else {
+            issue_block(0);
+            if (nblk > 1)
+                issue_block(1);
+            MLA_WAIT_VMCNT(0);
+            __syncthreads();
+
+            floatx4 o[kNS][8];
+#pragma unroll
+            for (int sh = 0; sh < kNS; ++sh)
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt)
+                    o[sh][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+            // token quads [ks0, ks1) of block j's second product
+            auto o_quads = [&](int j, auto ks0, auto ks1) {
+                const float *cs = s_c + (j % kRing) * kSlot;
+                const float *pp = s_p + (j & 1) * HT * kPRow;
+#pragma unroll
+                for (int ks = decltype(ks0)::value; ks < decltype(ks1)::value; ++ks) {
+                    const int row = 4 * ks + g;
+                    float pbv[kNS];
+#pragma unroll
+                    for (int sh = 0; sh < kNS; ++sh)
+                        pbv[sh] = pp[(16 * sh + l16) * kPRow + row];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const floatx4 a = *(const floatx4 *)(cs + slot_at(row, 32 * w4 + 16 * h + l16));
+#pragma unroll
+                        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                            for (int sh = 0; sh < kNS; ++sh)
+                                o[sh][4 * h + tt] = mfma16x16x4f32(a[tt], pbv[sh], o[sh][4 * h + tt]);
+                    }
+                }
+            };
+            for (int t = 0; t <= nblk; ++t) {
+#ifdef MLA_TIMELINE
+                tm = MLA_MT32();
+#endif
+                // block t + 2 into the slot that block t - 2 left at the end
+                // of the previous step (the O waves' share)
+                if (t + 2 < nblk)
+                    issue_block(t + 2);
+                if (t >= 1) {
+                    // ---- O^T += C_N^T P^T of block t - 1 (rescaled by its alpha first)
+#pragma unroll
+                    for (int sh = 0; sh < kNS; ++sh) {
+                        const float alpha = s_alpha[((t - 1) & 1) * HT + 16 * sh + l16];
+#pragma unroll
+                        for (int dt = 0; dt < 8; ++dt)
+                            o[sh][dt] *= alpha;
+                    }
+                    o_quads(t - 1, std::integral_constant<int, 0>{}, std::integral_constant<int, kQuadsA>{});
+                }
+#ifdef MLA_TIMELINE
+                wk_a += MLA_MT32() - tm;
+                tm = MLA_MT32();
+#endif
+                __syncthreads();  // barrier X
+                if (t >= 1)
+                    o_quads(t - 1, std::integral_constant<int, kQuadsA>{}, std::integral_constant<int, 4>{});
+                if (t + 2 < nblk)
+                    MLA_WAIT_VMCNT(kLoadsO);
                 else
-                    stage[s] = floatx4{0.f, 0.f, 0.f, 0.f};
-            }
-        };
-        auto store_stage = [&](int which) {
-            float *dst = s_c + which * kBT * kRow;
-#pragma unroll
-            for (int s = 0; s < kStage; ++s) {
-                const int ci = tid + 256 * s;
-                const int tok = ci / kRowChunks;
-                const int col = ci - tok * kRowChunks;
-                *(floatx4 *)(dst + tok * kRow + col * 4) = stage[s];
-            }
-        };
-
-        load_stage(p_lo);
-        store_stage(0);
-        if (nblk > 1)
-            load_stage(p_lo + kBT);
-
-        float m_run = -INFINITY, l_run = 0.f;
-        floatx4 o[8];
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-        __syncthreads();
-        MLA_STAMP32(1, __builtin_amdgcn_s_memrealtime());
-        MLA_STAMP32(11, nblk);
-
-        for (int blk = 0; blk < nblk; ++blk) {
+                    MLA_WAIT_VMCNT(0);
 #ifdef MLA_TIMELINE
-            tm = MLA_MT32();
+                wk_b += MLA_MT32() - tm;
 #endif
-            const int cur = blk & 1;
-            const int t0 = p_lo + blk * kBT;
-            const float *cs = s_c + cur * kBT * kRow;
-
-            // ---- partial S^T over this wave's K-quarter
-            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-            {
-                const float *arow = cs + l16 * kRow + kKQ * wave + 4 * g;
-#pragma unroll
-                for (int kq = 0; kq < kKQ / 16; ++kq) {
-                    const floatx4 a = *(const floatx4 *)(arow + 16 * kq);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc = mfma16x16x4f32(a[j], qf[kq][j], acc);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                s_s[(wave * kBT + 4 * g + i) * kSRow + l16] = acc[i];
-            __syncthreads();
-#ifdef MLA_TIMELINE
-            { const unsigned long long t2 = MLA_MT32(); ph_s += t2 - tm; tm = t2; }
-#endif
-
-            // ---- full tile, softmax (every wave, identical results)
-            float sv[4];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = (4 * g + i) * kSRow + l16;
-                const float sdot = ((s_s[r] + s_s[kBT * kSRow + r]) + s_s[2 * kBT * kSRow + r]) + s_s[3 * kBT * kSRow + r];
-                sv[i] = (t0 + 4 * g + i) < p_hi ? sdot * scale_log2 : -INFINITY;
-                mx = fmaxf(mx, sv[i]);
-            }
-            mx = max_over_lane_groups(mx);
-            const float mn = fmaxf(m_run, mx);
-            const float alpha = fast_exp2(m_run - mn);
-            m_run = mn;
-            float psum = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = fast_exp2(sv[i] - mn);
-                psum += p;
-                if (wave == 0)
-                    s_p[l16 * kPRow + 4 * g + i] = p;
-            }
-            l_run = l_run * alpha + psum;
-
-            if (blk + 1 < nblk)
-                store_stage(cur ^ 1);
-            if (blk + 2 < nblk)
-                load_stage(t0 + 2 * kBT);
-            __syncthreads();
-#ifdef MLA_TIMELINE
-            { const unsigned long long t2 = MLA_MT32(); ph_x += t2 - tm; tm = t2; }
-#endif
-
-            // ---- O^T[dims 128*wave .. +128][heads] += C_N^T P^T; o[4h + t]
-            // row i is dim 128*wave + 64h + 4i + t
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt)
-                o[dt] *= alpha;
-#pragma unroll
-            for (int ks = 0; ks < kBT / 4; ++ks) {
-                const float pbv = s_p[l16 * kPRow + 4 * ks + g];
-                const float *crow = cs + (4 * ks + g) * kRow + 128 * wave + 4 * l16;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const floatx4 a = *(const floatx4 *)(crow + 64 * h);
-#pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        o[4 * h + t] = mfma16x16x4f32(a[t], pbv, o[4 * h + t]);
-                }
+                __syncthreads();  // barrier Y
             }
 #ifdef MLA_TIMELINE
-            { const unsigned long long t2 = MLA_MT32(); ph_o += t2 - tm; }
+            MLA_STAMP32W(4, 9, wk_a);
+            MLA_STAMP32W(4, 10, wk_b);
 #endif
+            // in the MFMA accumulator order of natural 16 x 16 tiles (frag_offset):
+            // lane (head j, g) holds, over o[sh][4h .. 4h+3], dims 16g .. 16g+15 of
+            // tile 8*w4 + 4h + g of sub-tile sh, element r of o[sh][4h + t]
+            // being dim 4r + t of it; each store writes 4 runs of 256
+            // contiguous bytes. Nontemporal, as the partials are read once,
+            // by the combine (see mla_splitkv_fp16.hip)
+            float *obase = o_part + (size_t)slot * num_heads * kDV;
+#pragma unroll
+            for (int sh = 0; sh < kNS; ++sh)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const floatx4 v = {o[sh][4 * h][r], o[sh][4 * h + 1][r], o[sh][4 * h + 2][r],
+                                           o[sh][4 * h + 3][r]};
+                        __builtin_nontemporal_store(
+                            v, (floatx4 *)(obase + frag_offset(head0 + 16 * sh + l16,
+                                                               128 * w4 + 64 * h + 16 * g + 4 * r)));
+                    }
         }
-        MLA_STAMP32(2, __builtin_amdgcn_s_memrealtime());
-#ifdef MLA_TIMELINE
-        MLA_STAMP32(6, ph_s);
-        MLA_STAMP32(7, ph_x);
-        MLA_STAMP32(8, ph_o);
-#endif
-
-        const float lsum = sum_over_lane_groups(l_run);
-        if (tid < kHT) {
-            __builtin_nontemporal_store(m_run, m_part + (size_t)slot * num_heads + head0 + tid);
-            __builtin_nontemporal_store(lsum, l_part + (size_t)slot * num_heads + head0 + tid);
-        }
-        // in the MFMA accumulator order of natural 16 x 16 tiles (frag_offset):
-        // lane (head j, g) holds, over o[4h .. 4h+3], dims 16g .. 16g+15 of
-        // tile 8*wave + 4h + g, element r of o[4h + t] being dim 4r + t of
-        // it; each store writes 4 runs of 256 contiguous bytes. Nontemporal,
-        // as the partials are read once, by the combine (see
-        // mla_splitkv_fp16.hip)
-        float *obase = o_part + (size_t)slot * num_heads * kDV;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const floatx4 v = {o[4 * h][r], o[4 * h + 1][r], o[4 * h + 2][r], o[4 * h + 3][r]};
-                __builtin_nontemporal_store(
-                    v, (floatx4 *)(obase + frag_offset(head0 + l16, 128 * wave + 64 * h + 16 * g + 4 * r)));
-            }
 #ifdef MLA_TIMELINE
         MLA_WAIT_VMCNT(0);
 #endif
@@ -307,8 +431,10 @@ hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p, const Partials 
 {
     if (p.n_chunks == 0)
         return hipSuccess;
-    const dim3 grid(grid_chunks(p) * p.n_head_tiles), block(256);
-    hipLaunchKernelGGL(splitkv_fp32_kernel, grid, block, 0, s,
+    if (p.head_tile != 16 && p.head_tile != 32)
+        return hipErrorInvalidValue;
+    const dim3 grid(grid_chunks(p) * p.n_head_tiles), block(64 * kWaves);
+    hipLaunchKernelGGL(p.head_tile == 32 ? splitkv_fp32_kernel<32> : splitkv_fp32_kernel<16>, grid, block, 0, s,
                        (const float *)pb.q, (const float *)pb.c, pb.cu_seqlens,
                        static_cast<float *>(w.o), w.m, w.l, pb.num_heads, pb.batch, pb.total_tokens,
                        p.chunk, p.n_head_tiles, p.xcd_remap, pb.scale_log2);

@@ -31,11 +31,12 @@ the time from the split kernel's last partial store to the first combine
 wave's entry.
 
 --fp32 reads the fp32 kernel's stamps instead (calls through
-mla_decode_fused_fp32, so launch_us includes the combine): entry, first
-block, loop end and partials stored, and per 16-token block the shader cycles
-of wave 0's three phases -- the first product (to the barrier after the
-partial logits), the softmax and C staging (to the next barrier) and the
-second product.
+mla_decode_fused_fp32, so call_us includes the combine): entry, first
+block, loop end and partials stored, and per step (one 16-token block of
+each role: the S waves' block t, the O waves' block t - 1) the shader cycles
+of wave 0 (an S wave) in its three phases -- the partial first product (to
+barrier X), the softmax (to the wait for the next block's loads) and that
+wait with barrier Y.
 
 Usage (single sequences, inputs rotated over >= 1 GB so that C comes from HBM):
   python ada-mla_amd/timeline.py --heads 128 --tokens 65536 --splits 128 --head-tile 64
@@ -258,14 +259,19 @@ def run_case_f32(lib, torch, n_h, n, splits, k, spin_s):
         v = (x[:, e] - t0) * 0.01
         phases[name] = [round(float(np.median(v)), 2), round(float(v.min()), 2), round(float(v.max()), 2)]
     nblk = x[:, 11].astype(np.float64)
+    steps = nblk + 1  # the S waves run one block ahead of the O waves
     cyc = x[:, 6] + x[:, 7] + x[:, 8]
     clk = float(np.median(cyc / ((x[:, 2] - x[:, 1]) * 0.01 * 1e3)))
     rec = dict(path="fp32", heads=n_h, tokens=n, workgroups=int(len(x)), blocks=int(np.median(nblk)),
                call_us=round(us, 2), span_us=round(float((x[:, 3].max() - t0) * 0.01), 2), clock_ghz=round(clk, 3),
-               block_cycles=round(float(np.median(cyc / nblk))),
-               first_product_cycles=round(float(np.median(x[:, 6] / nblk))),
-               softmax_staging_cycles=round(float(np.median(x[:, 7] / nblk))),
-               second_product_cycles=round(float(np.median(x[:, 8] / nblk))),
+               step_cycles=round(float(np.median(cyc / steps))),
+               s_product_cycles=round(float(np.median(x[:, 6] / steps))),
+               s_softmax_cycles=round(float(np.median(x[:, 7] / steps))),
+               wait_barrier_cycles=round(float(np.median(x[:, 8] / steps))),
+               s_work_a_cycles=round(float(np.median(x[:, 4] / steps))),
+               s_work_b_cycles=round(float(np.median(x[:, 5] / steps))),
+               o_work_a_cycles=round(float(np.median(x[:, 9] / steps))),
+               o_work_b_cycles=round(float(np.median(x[:, 10] / steps))),
                phases_med_min_max_us=phases)
     del qs, cs, ws
     torch.cuda.empty_cache()

@@ -91,9 +91,10 @@ def test_fp32_shapes(n_h, n):
     _check32(_fp32(q, c), O.closed_form(q, c), f"n_h={n_h} N={n}")
 
 
-@pytest.mark.parametrize("n_h,n", [(128, 16384), (128, 20001), (32, 65536 + 7)])
-def test_fp32_two_workgroups_per_cu(n_h, n):
-    # long sequences: the fp32 plan puts two workgroups on each CU
+@pytest.mark.parametrize("n_h,n", [(128, 16384), (128, 20001), (32, 65536 + 7), (64, 32768 + 5), (48, 20000)])
+def test_fp32_long_sequences(n_h, n):
+    # long sequences: the fp32 plan takes 32-head workgroups where n_h allows
+    # (two 16-head sub-tiles per wave), 16-head ones at n_h = 48
     print(f"fp32 n_h={n_h} N={n}", flush=True)
     q, c = synthetic.decode_inputs(n_h, n, seed=300 + n)
     q, c = q.astype(np.float32), c.astype(np.float32)
