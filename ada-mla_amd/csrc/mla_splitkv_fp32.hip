@@ -188,11 +188,9 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
         // p = 64u + i is row p / 144, stored chunk p % 144, i.e. logical
         // chunk (p % 144) ^ (row mod 16). Rows past the piece repeat its last
         // token (their logits are masked).
-        auto issue_block = [&](int j) {
-            const int t0 = p_lo + j * kBT;
-            const float *base = c + (size_t)t0 * kDK;
-            const float *dst = s_c + (j % kRing) * kSlot;
-            const int last = p_hi - 1 - t0;
+        // 16 rows of 576 floats from base (rows past `last` repeat row
+        // `last`) into the ring slot at dst
+        auto issue_rows = [&](const float *base, int last, const float *dst) {
 #pragma unroll
             for (int k = 0; k < (s_role ? kLoadsS : kLoadsO); ++k) {
                 const int u = (s_role ? 4 * kLoadsO : 0) + w4 + 4 * k;
@@ -204,6 +202,30 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                 global_to_lds16(base, (src_row * kRowChunks + lch) * 16, dst + 256 * u);
             }
         };
+        auto issue_block = [&](int j) {
+            const int t0 = p_lo + j * kBT;
+            issue_rows(c + (size_t)t0 * kDK, p_hi - 1 - t0, s_c + (j % kRing) * kSlot);
+        };
+
+        // Prologue: Q* of the head tile (16 heads per sub-tile, swizzled like
+        // C rows) into ring slots 2 .. 2 + kNS - 1, blocks 0 and 1 into slots
+        // 0 and 1, all by direct loads; the block loop starts once Q* and
+        // block 0 have landed and the S waves hold Q* in registers. Q* does
+        // not pass through the compiler's own loads: it would count them,
+        // and not the direct loads issued after them, and then wait for them
+        // inside the block loop, where its vmcnt waits would drain the ring
+        // loads of block t + 2 at every step.
+#pragma unroll
+        for (int sh = 0; sh < kNS; ++sh)
+            issue_rows(q + ((size_t)b * num_heads + head0 + 16 * sh) * kDK, 15, s_c + (2 + sh) * kSlot);
+        issue_block(0);
+        if (nblk > 1) {
+            issue_block(1);
+            if (s_role) MLA_WAIT_VMCNT(kLoadsS); else MLA_WAIT_VMCNT(kLoadsO);
+        } else {
+            MLA_WAIT_VMCNT(0);
+        }
+        __syncthreads();
 
         // The two roles run separate loops with the same barriers (two per
         // step), so that the S waves' Q* and the O waves' accumulators share
@@ -213,22 +235,12 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
             floatx4 qf[kNS][kKQ / 16];
 #pragma unroll
             for (int sh = 0; sh < kNS; ++sh) {
-                const float *qrow = q + ((size_t)b * num_heads + head0 + 16 * sh + l16) * kDK + kKQ * w4 + 4 * g;
+                const float *qs = s_c + (2 + sh) * kSlot;
 #pragma unroll
                 for (int kq = 0; kq < kKQ / 16; ++kq)
-                    qf[sh][kq] = *(const floatx4 *)(qrow + 16 * kq);
+                    qf[sh][kq] = *(const floatx4 *)(qs + slot_at(l16, 36 * w4 + 4 * kq + g));
             }
-            issue_block(0);
-            if (nblk > 1)
-                issue_block(1);
-            // Q* in registers, blocks 0 and 1 landed. The wait is for every
-            // load: the compiler counts only its own loads (Q*), not the
-            // direct loads issued after them, so after a partial wait it would
-            // still take Q* as in flight and wait for it inside the block
-            // loop, where its vmcnt waits would then drain the ring loads of
-            // block t + 2 at every step.
-            MLA_WAIT_VMCNT(0);
-            __syncthreads();
+            __syncthreads();  // Q* read: slots 2 .. take blocks 2 .. from step 0 on
             MLA_STAMP32(1, __builtin_amdgcn_s_memrealtime());
             MLA_STAMP32(11, nblk);
 
@@ -325,11 +337,7 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                 __builtin_nontemporal_store(lsum, l_part + mi);
             }
         } else {
-            issue_block(0);
-            if (nblk > 1)
-                issue_block(1);
-            MLA_WAIT_VMCNT(0);
-            __syncthreads();
+            __syncthreads();  // the S waves' Q* reads
 
             floatx4 o[kNS][8];
 #pragma unroll
