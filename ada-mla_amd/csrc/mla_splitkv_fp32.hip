@@ -85,12 +85,20 @@ constexpr int kLoadsS = 4;
 static_assert(4 * (kLoadsO + kLoadsS) == kLoads, "load split");
 constexpr int kWaves = 8;
 constexpr int kKQ = kDK / 4;             // K per S wave (144)
-constexpr int kPRow = kBT + 4;
-// partial S^T tiles [wave][head][token] with rows of 20 floats: lane
-// (head j, g) writes and reads tokens 4g .. 4g + 3 of row j as one 16-byte
-// access, and the 16 rows of an instruction then fall on 16 distinct 4-bank
-// groups
-constexpr int kSRow = kBT + 4;
+// The small tiles exchanged through LDS at every step -- the partial S^T
+// tiles [wave][head][token] and P [head][token] -- have rows of 16 floats,
+// four 16-byte chunks, chunk k of row r stored at k ^ ((r >> 1) & 3). The
+// 16-byte accesses of lanes (row j, chunk g) are then free of bank
+// conflicts (measured on gfx950 with SQ_LDS_BANK_CONFLICT in probe kernels;
+// rows of 20 floats conflicted on the reads, 0.33 of LDS-active cycles).
+// P is stored quad-transposed: token 4 ks + g of head j is element ks of
+// chunk g of row j, so lane (j, g) of an O wave reads its tokens g, g + 4,
+// g + 8, g + 12 as one 16-byte chunk.
+constexpr int kTRow = 16;
+__device__ __forceinline__ int tile_at(int row, int chunk)
+{
+    return row * kTRow + 4 * (chunk ^ ((row >> 1) & 3));
+}
 static_assert(kRowChunks % 16 == 0, "the row swizzle stays within a row");
 static_assert(kLoads == 36, "block loads");
 
@@ -114,8 +122,8 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
     // S waves' softmax)
     constexpr int kQuadsA = kNS == 1 ? 1 : 2;
     __shared__ __attribute__((aligned(1024))) float s_c[kRing * kSlot];
-    __shared__ __attribute__((aligned(16))) float s_s[4 * HT * kSRow];
-    __shared__ __attribute__((aligned(16))) float s_p[2 * HT * kPRow];
+    __shared__ __attribute__((aligned(16))) float s_s[4 * HT * kTRow];
+    __shared__ __attribute__((aligned(16))) float s_p[2 * HT * kTRow];
     __shared__ float s_alpha[2 * HT];
 
     const int tid = threadIdx.x;
@@ -267,7 +275,7 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                     }
 #pragma unroll
                     for (int sh = 0; sh < kNS; ++sh)
-                        *(floatx4 *)(s_s + (w4 * HT + 16 * sh + l16) * kSRow + 4 * g) = acc[sh];
+                        *(floatx4 *)(s_s + tile_at(w4 * HT + 16 * sh + l16, g)) = acc[sh];
                 }
 #ifdef MLA_TIMELINE
                 wk_a += MLA_MT32() - tm;
@@ -280,10 +288,10 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                     // ---- full tile and softmax of sub-tile my_sh (every S
                     // wave of the sub-tile, identical results)
                     const int t0 = p_lo + t * kBT;
-                    const float *sp = s_s + (16 * my_sh + l16) * kSRow + 4 * g;
-                    const floatx4 sdot = ((*(const floatx4 *)sp + *(const floatx4 *)(sp + HT * kSRow)) +
-                                          *(const floatx4 *)(sp + 2 * HT * kSRow)) +
-                                         *(const floatx4 *)(sp + 3 * HT * kSRow);
+                    const float *sp = s_s + tile_at(16 * my_sh + l16, g);  // (the swizzle repeats every 16 rows)
+                    const floatx4 sdot = ((*(const floatx4 *)sp + *(const floatx4 *)(sp + HT * kTRow)) +
+                                          *(const floatx4 *)(sp + 2 * HT * kTRow)) +
+                                         *(const floatx4 *)(sp + 3 * HT * kTRow);
                     float sv[4];
                     float mx = -INFINITY;
 #pragma unroll
@@ -301,7 +309,11 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                         pv[i] = fast_exp2(sv[i] - mn);
                     l_run = l_run * alpha + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
                     if (w4 < kNS) {
-                        *(floatx4 *)(s_p + (t & 1) * HT * kPRow + (16 * my_sh + l16) * kPRow + 4 * g) = pv;
+                        // token 4g + i is element g of chunk i (quad-transposed)
+                        float *pw = s_p + (t & 1) * HT * kTRow;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            pw[tile_at(16 * my_sh + l16, i) + g] = pv[i];
                         if (g == 0)
                             s_alpha[(t & 1) * HT + 16 * my_sh + l16] = alpha;
                     }
@@ -345,17 +357,14 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt)
                     o[sh][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+            // P of block j for this lane's tokens g, g + 4, g + 8, g + 12
+            floatx4 pq[kNS];
             // token quads [ks0, ks1) of block j's second product
             auto o_quads = [&](int j, auto ks0, auto ks1) {
                 const float *cs = s_c + (j % kRing) * kSlot;
-                const float *pp = s_p + (j & 1) * HT * kPRow;
 #pragma unroll
                 for (int ks = decltype(ks0)::value; ks < decltype(ks1)::value; ++ks) {
                     const int row = 4 * ks + g;
-                    float pbv[kNS];
-#pragma unroll
-                    for (int sh = 0; sh < kNS; ++sh)
-                        pbv[sh] = pp[(16 * sh + l16) * kPRow + row];
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         const floatx4 a = *(const floatx4 *)(cs + slot_at(row, 32 * w4 + 16 * h + l16));
@@ -363,7 +372,7 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                         for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
                             for (int sh = 0; sh < kNS; ++sh)
-                                o[sh][4 * h + tt] = mfma16x16x4f32(a[tt], pbv[sh], o[sh][4 * h + tt]);
+                                o[sh][4 * h + tt] = mfma16x16x4f32(a[tt], pq[sh][ks], o[sh][4 * h + tt]);
                     }
                 }
             };
@@ -379,6 +388,7 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
                     // ---- O^T += C_N^T P^T of block t - 1 (rescaled by its alpha first)
 #pragma unroll
                     for (int sh = 0; sh < kNS; ++sh) {
+                        pq[sh] = *(const floatx4 *)(s_p + ((t - 1) & 1) * HT * kTRow + tile_at(16 * sh + l16, g));
                         const float alpha = s_alpha[((t - 1) & 1) * HT + 16 * sh + l16];
 #pragma unroll
                         for (int dt = 0; dt < 8; ++dt)
