@@ -684,9 +684,18 @@ void splitkv_fp16_kernel(const E *__restrict__ q,
             return intx8{(int)x.x, (int)x.y, (int)x.z, (int)x.w, (int)y.x, (int)y.y, (int)y.z, (int)y.w};
         };
 
+#ifdef MLA_TIMELINE
+        int tl_blocks = 0, tl_pieces = 0;  // the workgroup's blocks and pieces over its chunk
+#endif
         for_each_piece([&](int b, int seq_lo, int p_org, int p_lo, int p_hi) {
             const int slot_out = split + b;
             const int nblk = (p_hi - p_org + T::kBT - 1) / T::kBT;
+#ifdef MLA_TIMELINE
+            tl_blocks += nblk;
+            ++tl_pieces;
+            MLA_STAMP(0, 14, tl_blocks);
+            MLA_STAMP(0, 15, tl_pieces);
+#endif
             piece_prologue(b, seq_lo, p_org, p_hi);
             MLA_STAMP(0, 1, MLA_RT());
             lds_barrier();  // A: Q* (split, with kF8M) and block 0 have landed

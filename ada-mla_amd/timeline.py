@@ -129,36 +129,47 @@ def run_case(lib, torch, n_h, n, splits, flags, k, spin_s):
     return rec
 
 
-def run_case_combine(lib, torch, n_h, n, splits, flags, k, spin_s):
-    """Whole calls (split kernel, then combine_kernel): the split kernel's
-    stamps and the combine's per-wave stamps of the last call, both relative
-    to the split kernel's first workgroup entry."""
+def run_case_combine(lib, torch, n_h, n, splits, flags, k, spin_s, seqlens=None):
+    """Whole calls (split kernel, then the combine): the split kernel's stamps
+    and the combine's per-wave stamps of the last call, both relative to the
+    split kernel's first workgroup entry. With seqlens, a batch of sequences
+    of those lengths (packed, mla_decode_split_batched_fp16; n is then their
+    total)."""
     import numpy as np
     vp = ctypes.c_void_p
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     sp = vp(stream.cuda_stream)
-    set_bytes = n * 576 * 2 + n_h * 576 * 2
+    batch = 1 if seqlens is None else len(seqlens)
+    set_bytes = n * 576 * 2 + batch * n_h * 576 * 2
     pool = min(64, max(2, math.ceil(1024 * 2**20 / set_bytes) + 1))
-    qs = [torch.randn(n_h, 576, device=dev, dtype=torch.float16) for _ in range(pool)]
+    qs = [torch.randn(batch, n_h, 576, device=dev, dtype=torch.float16) for _ in range(pool)]
     cs = [torch.randn(n, 576, device=dev, dtype=torch.float16) for _ in range(pool)]
-    out = torch.empty(n_h, 512, device=dev, dtype=torch.float16)
-    wsb = lib.mla_decode_split_workspace_size(n_h, n, splits)
+    out = torch.empty(batch, n_h, 512, device=dev, dtype=torch.float16)
+    if seqlens is None:
+        wsb = lib.mla_decode_split_workspace_size(n_h, n, splits)
+        if lib.mla_decode_split_launches(n_h, n, splits, flags) != 2:
+            raise SystemExit("this plan makes one launch (no combine)")
+        ht = lib.mla_decode_split_head_tile(n_h, n, splits, flags)
+        ns = lib.mla_decode_split_num_splits(n_h, n, splits, flags)
+    else:
+        cu = torch.tensor(np.concatenate([[0], np.cumsum(seqlens)]).astype(np.int32), device=dev)
+        wsb = lib.mla_decode_split_batched_workspace_size(batch, n_h, n, splits)
+        ht = ns = 0  # not reported for batches
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
-    ht = lib.mla_decode_split_head_tile(n_h, n, splits, flags)
-    ns = lib.mla_decode_split_num_splits(n_h, n, splits, flags)
-    if lib.mla_decode_split_launches(n_h, n, splits, flags) != 2:
-        raise SystemExit("this plan makes one launch (no combine)")
-    n_wg = ((ns + 7) // 8 * 8) * (n_h // ht)
     cursor = [0]
 
     def launch():
         i = cursor[0] % pool
         cursor[0] += 1
-        st = lib.mla_decode_split_fp16_ex(qs[i].data_ptr(), cs[i].data_ptr(), out.data_ptr(), ws.data_ptr(), wsb,
-                                          n_h, n, splits, flags, sp)
+        if seqlens is None:
+            st = lib.mla_decode_split_fp16_ex(qs[i].data_ptr(), cs[i].data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                              wsb, n_h, n, splits, flags, sp)
+        else:
+            st = lib.mla_decode_split_batched_fp16(qs[i].data_ptr(), cs[i].data_ptr(), cu.data_ptr(),
+                                                   out.data_ptr(), ws.data_ptr(), wsb, batch, n_h, n, splits, sp)
         if st != 0:
-            raise RuntimeError(f"mla_decode_split_fp16_ex: status {st}")
+            raise RuntimeError(f"decode call: status {st}")
 
     t_end = time.perf_counter() + spin_s
     while time.perf_counter() < t_end:
@@ -179,11 +190,12 @@ def run_case_combine(lib, torch, n_h, n, splits, flags, k, spin_s):
     launch()  # the call whose stamps are read, after back-to-back ones
     launch()
     torch.cuda.synchronize()
-    buf = np.zeros(n_wg * SLOTS, dtype=np.uint64)
+    buf = np.zeros(8192 * SLOTS, dtype=np.uint64)
     if lib.mla_timeline_read(buf.ctypes.data, buf.nbytes) != 0:
         raise RuntimeError("mla_timeline_read failed")
-    x = buf.reshape(n_wg, SLOTS).astype(np.int64)
-    x = x[x[:, 10] > x[:, 0]]
+    x = buf.reshape(8192, SLOTS).astype(np.int64)
+    x = x[(x[:, 10] > x[:, 0]) & (x[:, 0] > 0)]
+    x = x[x[:, 0] >= x[:, 0].max() - 100000]  # the last call's workgroups (within 1 ms of its last entry)
     cb = np.zeros(16384 * 4, dtype=np.uint64)
     if lib.mla_timeline_read_combine(cb.ctypes.data, cb.nbytes) != 0:
         raise RuntimeError("mla_timeline_read_combine failed")
@@ -196,7 +208,20 @@ def run_case_combine(lib, torch, n_h, n, splits, flags, k, spin_s):
         v = (v - t0) * 0.01
         return [round(float(np.median(v)), 2), round(float(v.min()), 2), round(float(v.max()), 2)]
 
-    rec = dict(heads=n_h, tokens=n, head_tile=int(ht), splits=int(ns),
+    if seqlens is not None:
+        # the split kernel's workgroups by work (blocks and pieces over the chunk) against their end time
+        end = (np.maximum(x[:, 10], x[:, 5]) - t0) * 0.01
+        blocks, pieces = x[:, 14], x[:, 15]
+        order = np.argsort(end)
+        def row(i):
+            return [round(float(end[i]), 2), int(blocks[i]), int(pieces[i])]
+        print(json.dumps(dict(split_end_blocks_pieces_first5=[row(i) for i in order[:5]],
+                              last5=[row(i) for i in order[-5:]],
+                              corr_end_blocks=round(float(np.corrcoef(end, blocks)[0, 1]), 3),
+                              corr_end_pieces=round(float(np.corrcoef(end, pieces)[0, 1]), 3),
+                              blocks_min_max=[int(blocks.min()), int(blocks.max())],
+                              pieces_min_max=[int(pieces.min()), int(pieces.max())])), flush=True)
+    rec = dict(heads=n_h, tokens=n, batch=batch, head_tile=int(ht), splits=int(ns),
                partials="fp32" if flags & FLAG_FP32_PARTIALS else "fp16", call_us=round(us, 2),
                split_workgroups=int(len(x)), combine_waves=int(len(c)),
                split_entry=mmm(x[:, 0]), split_stored=mmm(np.maximum(x[:, 10], x[:, 5])),
@@ -291,6 +316,8 @@ def main():
     ap.add_argument("--fp32", action="store_true", help="the fp32 kernel (mla_decode_fused_fp32)")
     ap.add_argument("--combine", action="store_true",
                     help="whole calls: the split kernel's end and the combine's per-wave stamps")
+    ap.add_argument("--batch-config5", action="store_true",
+                    help="with --combine: the batched workload (B = 32, BASELINE config-5 lengths)")
     args = ap.parse_args()
     if not os.path.exists(LIB):
         raise SystemExit(f"{LIB} is not built (python ada-mla_amd/build.py --timeline)")
@@ -317,6 +344,16 @@ def main():
             print(json.dumps(run_case_f32(lib, torch, args.heads, n, args.splits, args.calls, args.spin_s)), flush=True)
         return 0
     flags = FLAG_FP32_PARTIALS if args.partials == "fp32" else 0
+    lib.mla_decode_split_batched_workspace_size.restype = sz
+    lib.mla_decode_split_batched_workspace_size.argtypes = [i_, i_, i_, i_]
+    lib.mla_decode_split_batched_fp16.argtypes = [vp, vp, vp, vp, vp, sz, i_, i_, i_, i_, vp]
+    if args.combine and args.batch_config5:
+        sys.path.insert(0, HERE)
+        from ada_mla import synthetic
+        lens = synthetic.batched_seqlens(32, seed=42)
+        print(json.dumps(run_case_combine(lib, torch, args.heads, int(lens.sum()), args.splits, 0, args.calls,
+                                          args.spin_s, seqlens=lens)), flush=True)
+        return 0
     if args.combine:
         for n in (int(t) for t in args.tokens.split(",")):
             print(json.dumps(run_case_combine(lib, torch, args.heads, n, args.splits, flags, args.calls,
