@@ -9,33 +9,37 @@
 // split so the grid fills the GPU, and the splits are merged by
 // mla_combine.hip.
 //
-// Workgroup = 8 wave64s (two per SIMD), 16 heads, blocks of 16 tokens, in
-// two roles pipelined one block apart: at step t the S waves form the logits
-// and the softmax of block t while the O waves add block t - 1 into O, so
-// one wave's softmax and LDS traffic overlap the other's MFMAs on each SIMD.
+// Workgroup = 8 wave64s (two per SIMD), 16 or 32 heads (one or two 16-head
+// sub-tiles carried by every wave), blocks of 16 tokens, in two roles
+// pipelined one block apart: at step t the S waves form the logits and the
+// softmax of block t while the O waves add block t - 1 into O, so one wave's
+// softmax and LDS traffic overlap the other's MFMAs on each SIMD. The roles
+// run separate loops with the same two barriers per step.
 //  * S waves 0..3: S^T = C Q*^T, wave w owning K-quarter [144w, 144w + 144)
-//    of the 16x16 tile (its Q* slice stays in VGPRs); the four partial tiles
-//    are summed through LDS (barrier X), and every S wave redoes the (tiny)
-//    softmax, so all of them hold the running max and sum; wave 0 publishes P
-//    and the rescale factor of each head for the O waves. Each lane reads 4
-//    consecutive K of both operands with one 16-byte LDS read and feeds them
-//    to 4 MFMAs (the same K permutation on A and B).
+//    of each 16x16 tile (its Q* slices stay in VGPRs); the four partial tiles
+//    are summed through LDS (barrier X), and every S wave of a sub-tile
+//    redoes its (tiny) softmax, so all of them hold the running max and sum;
+//    one publishes P and the rescale factor of each head for the O waves.
+//    Each lane reads 4 consecutive K of both operands with one 16-byte LDS
+//    read and feeds them to 4 MFMAs per sub-tile (the same K permutation on A
+//    and B).
 //  * O waves 4..7: O^T = C_N^T P^T, wave 4 + w owning 128 output columns,
 //    read from LDS as 16-byte runs: MFMA tile t (0..3) of half h takes as its
 //    row i the value dim 128w + 64h + 4i + t, so one ds_read_b128 of dims
 //    128w + 64h + 4i .. +3 feeds four MFMAs and the 16 lanes of a token row
 //    read 256 contiguous bytes. The store undoes the permutation: lane
 //    (head j, g) of the four tiles holds the 16 dims of natural tile
-//    8w + 4h + g. An O wave runs one of its block's four token quads before
-//    barrier X and three after, so that its MFMAs fill the S wave's softmax
-//    on the same SIMD.
+//    8w + 4h + g. An O wave runs one of its block's four token quads (two at
+//    32 heads) before barrier X and the rest after it, so that its MFMAs fill
+//    the S wave's softmax on the same SIMD.
 //  * C blocks go HBM -> LDS by the direct global->LDS load (36 loads of 1 KB
 //    per block: 20 issued by the O waves before their MFMAs, 16 by the S
 //    waves after their softmax) into a 4-slot ring, two blocks ahead of the
-//    S waves; rows are 2304 bytes with 16-byte chunk c of row r
-//    at c ^ (r mod 16), so the S waves' row reads (16 rows, one chunk) and
-//    the O waves' token-row reads (16 chunks of one row) both touch 16
-//    distinct chunk positions of a 256-byte bank period.
+//    S waves; Q* comes through ring slots 2 (and 3) the same way at the
+//    start of a piece. Rows are 2304 bytes with 16-byte chunk c of row r at
+//    c ^ (r mod 16), so the S waves' row reads (16 rows, one chunk) and the
+//    O waves' token-row reads (16 chunks of one row) both touch 16 distinct
+//    chunk positions of a 256-byte bank period.
 #include <type_traits>
 
 #include "mla_device.hpp"
@@ -46,11 +50,12 @@ namespace mla {
 
 #ifdef MLA_TIMELINE
 // Timeline build only (see mla_splitkv_fp16.hip): per workgroup of the fp32
-// kernel, wave 0 records s_memrealtime at entry, at the first block, at the
-// end of the block loop and after the partial store (stores complete), and
-// s_memtime sums over the blocks of its three phases: the first product (to
-// the barrier after the partial logits), the softmax and C staging (to the
-// next barrier) and the second product.
+// kernel, wave 0 (an S wave) records s_memrealtime at entry (slot 0), at the
+// first step (1), at the end of the step loop (2) and after its stores
+// complete (3), the block count (11), and s_memtime sums over the steps: to
+// barrier X (6), from X to the wait before barrier Y (7), that wait and Y
+// (8), and its own work before X (4) and after it (5); wave 4 (an O wave)
+// records its own work before X (9) and after it (10).
 constexpr int kTimelineWorkgroupsF32 = 8192;
 __device__ unsigned long long mla_timeline_stamps_f32[kTimelineWorkgroupsF32 * 16];
 #define MLA_STAMP32W(w, e, v)                                                              \
