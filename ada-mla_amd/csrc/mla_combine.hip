@@ -24,6 +24,9 @@
 //    instead merges 4 consecutive tiles of a sequence (same heads), so one
 //    m / l load serves 4 tiles and the grid runs in one round
 //    (combine_tiles_kernel).
+//  * with fewer items than CUs (one sequence at fewer than 128 heads), the
+//    unit is a quarter tile (16 heads x 4 dims), so four times as many
+//    workgroups share the reads (combine_quarter_kernel).
 //  * the kernels' arguments (14 dwords) are preloaded into SGPRs at wave
 //    launch (the library is built with -amdgpu-kernarg-preload-count=16), so
 //    the first loads do not wait for a kernel-argument fetch.
