@@ -101,6 +101,24 @@ def test_fp32_long_sequences(n_h, n):
     _check32(_fp32(q, c), O.closed_form(q, c), f"n_h={n_h} N={n}")
 
 
+@pytest.mark.parametrize("n_h", [32, 128])
+def test_fp32_split_count_invariance(n_h):
+    # requested split counts walk the fp32 kernel through both head tiles
+    # (32 heads once a chunk holds >= 192 tokens: 1, 2, 3, 7 splits here),
+    # one-block pieces (200 splits: 16-token chunks, the S and O roles each
+    # idle for one of the two steps) and a ragged last block (N = 3001)
+    q, c = synthetic.decode_inputs(n_h, 3001, seed=33)
+    q, c = q.astype(np.float32), c.astype(np.float32)
+    ref = O.closed_form(q, c)
+    outs = []
+    for s in [1, 2, 3, 7, 16, 64, 200]:
+        print(f"fp32 n_h={n_h} splits={s}", flush=True)
+        outs.append(_fp32(q, c, num_splits=s))
+        _check32(outs[-1], ref, f"n_h={n_h} splits={s}")
+    for o in outs[1:]:
+        assert np.abs(o - outs[0]).max() < 1e-5
+
+
 @pytest.mark.parametrize("n_h", [1024, 4096])
 @pytest.mark.parametrize("n", [1, 200])
 def test_many_heads(n_h, n):
