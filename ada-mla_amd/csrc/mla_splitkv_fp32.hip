@@ -124,8 +124,11 @@ void splitkv_fp32_kernel(const float *__restrict__ q,
 {
     constexpr int kNS = HT / 16;          // 16-head sub-tiles
     // O waves' token quads before barrier X (the rest after it, beside the
-    // S waves' softmax)
-    constexpr int kQuadsA = kNS == 1 ? 1 : 2;
+    // S waves' softmax). A SIMD's S and O waves share one MFMA pipe (one
+    // fp32 16x16x4 per 32 cycles), so quads moved before X only lengthen that
+    // phase; after X they hide the softmax. 32-head tiles run all four after
+    // X; 16-head tiles measure the same with one quad before it.
+    constexpr int kQuadsA = kNS == 1 ? 1 : 0;
     __shared__ __attribute__((aligned(1024))) float s_c[kRing * kSlot];
     __shared__ __attribute__((aligned(16))) float s_s[4 * HT * kTRow];
     __shared__ __attribute__((aligned(16))) float s_p[2 * HT * kTRow];
