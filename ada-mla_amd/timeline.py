@@ -194,8 +194,11 @@ def run_case_combine(lib, torch, n_h, n, splits, flags, k, spin_s, seqlens=None)
     if lib.mla_timeline_read(buf.ctypes.data, buf.nbytes) != 0:
         raise RuntimeError("mla_timeline_read failed")
     x = buf.reshape(8192, SLOTS).astype(np.int64)
-    x = x[(x[:, 10] > x[:, 0]) & (x[:, 0] > 0)]
-    x = x[x[:, 0] >= x[:, 0].max() - 100000]  # the last call's workgroups (within 1 ms of its last entry)
+    bid = np.arange(len(x))  # the stamp row is the workgroup id
+    keep = (x[:, 10] > x[:, 0]) & (x[:, 0] > 0)
+    x, bid = x[keep], bid[keep]
+    keep = x[:, 0] >= x[:, 0].max() - 100000  # the last call's workgroups (within 1 ms of its last entry)
+    x, bid = x[keep], bid[keep]
     cb = np.zeros(16384 * 4, dtype=np.uint64)
     if lib.mla_timeline_read_combine(cb.ctypes.data, cb.nbytes) != 0:
         raise RuntimeError("mla_timeline_read_combine failed")
@@ -208,7 +211,7 @@ def run_case_combine(lib, torch, n_h, n, splits, flags, k, spin_s, seqlens=None)
         v = (v - t0) * 0.01
         return [round(float(np.median(v)), 2), round(float(v.min()), 2), round(float(v.max()), 2)]
 
-    if seqlens is not None:
+    if True:
         # the split kernel's workgroups by work (blocks and pieces over the chunk) against their end time
         end = (np.maximum(x[:, 10], x[:, 5]) - t0) * 0.01
         blocks, pieces = x[:, 14], x[:, 15]
@@ -221,6 +224,19 @@ def run_case_combine(lib, torch, n_h, n, splits, flags, k, spin_s, seqlens=None)
                               corr_end_pieces=round(float(np.corrcoef(end, pieces)[0, 1]), 3),
                               blocks_min_max=[int(blocks.min()), int(blocks.max())],
                               pieces_min_max=[int(pieces.min()), int(pieces.max())])), flush=True)
+        # time per block from entry to the last store, by XCD (workgroup id mod 8: the dispatcher's
+        # round-robin) and by the workgroup's place among its chunk's head tiles (id / 8 mod the
+        # tile count, 2 at 64-head tiles of 128 heads)
+        per_blk = (end - (x[:, 0] - t0) * 0.01) / np.maximum(blocks, 1)
+        def by(key, n):
+            return [round(float(np.median(per_blk[key == i])), 3) if np.any(key == i) else None for i in range(n)]
+        n_tiles = max(1, n_h // 64)
+        print(json.dumps(dict(us_per_block_median=round(float(np.median(per_blk)), 3),
+                              us_per_block_min_max=[round(float(per_blk.min()), 3), round(float(per_blk.max()), 3)],
+                              us_per_block_by_xcd=by(bid & 7, 8),
+                              us_per_block_by_head_tile=by((bid >> 3) % n_tiles, n_tiles),
+                              entry_us_min_max=[round(float((x[:, 0].min() - t0) * 0.01), 2),
+                                                round(float((x[:, 0].max() - t0) * 0.01), 2)])), flush=True)
     rec = dict(heads=n_h, tokens=n, batch=batch, head_tile=int(ht), splits=int(ns),
                partials="fp32" if flags & FLAG_FP32_PARTIALS else "fp16", call_us=round(us, 2),
                split_workgroups=int(len(x)), combine_waves=int(len(c)),
