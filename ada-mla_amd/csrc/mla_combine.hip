@@ -24,9 +24,9 @@
 //    instead merges 4 consecutive tiles of a sequence (same heads), so one
 //    m / l load serves 4 tiles and the grid runs in one round
 //    (combine_tiles_kernel).
-//  * with fewer items than CUs (one sequence at fewer than 128 heads), the
-//    unit is a quarter tile (16 heads x 4 dims), so four times as many
-//    workgroups share the reads (combine_quarter_kernel).
+//  * with fewer items than CUs (one sequence at fewer than 128 heads), and
+//    with fp32 partials, the unit is a quarter tile (16 heads x 4 dims), so
+//    four times as many workgroups share the reads (combine_quarter_kernel).
 //  * the kernels' arguments (14 dwords) are preloaded into SGPRs at wave
 //    launch (the library is built with -amdgpu-kernarg-preload-count=16), so
 //    the first loads do not wait for a kernel-argument fetch.
@@ -379,7 +379,8 @@ void combine_tiles_kernel(const PartT *__restrict__ o_part,
 }
 
 // Few items (fewer (tile, sequence) items than CUs: one sequence at fewer
-// than 128 heads, small batches of few heads): the unit of work is a quarter
+// than 128 heads, small batches of few heads), or fp32 partials (up to
+// kResidentWaves items): the unit of work is a quarter
 // tile -- the 16 heads x 4 dims that lanes 16 q .. 16 q + 15 own in the
 // tile's accumulator order, 64 contiguous elements of each slot -- so the
 // grid holds four times as many workgroups and spreads the reads over that
@@ -625,8 +626,14 @@ extern "C" int mla_timeline_clear_combine()
 // items, about 5 slots each) merges in 8.4 us with one wave per item against
 // 12.4 us with two; one sequence (256 items) is fastest with the 4-slot
 // rule (N = 4096: 8 waves per item).
-// With fewer items than CUs, quarter items (combine_quarter_kernel, returned
-// as -W): W waves such that each merges about kUQ quads of slots, at most 16.
+// With fewer items than CUs, and with fp32 partials, quarter items
+// (combine_quarter_kernel, returned as -W): W waves such that each merges
+// about kUQ quads of slots, at most 16. fp32 partials read faster that way
+// at every slot count measured (one sequence at 128 heads, µs per call,
+// items -> quarter items: fp16 path with fp32 partials N = 4096 13.92 ->
+// 13.11, N = 16384 22.33 -> 21.01, N = 65536 35.02 -> 34.75; fp32 path
+// N = 1024 14.29 -> 13.59, N = 4096 24.78 -> 23.44, N = 8192 36.11 -> 35.62);
+// fp16 partials do not (N = 4096 10.79 -> 11.03).
 constexpr int kResidentWaves = 4096;
 
 int combine_waves_per_item(const Plan &p, int batch, int n_items, int cu_count)
@@ -634,7 +641,7 @@ int combine_waves_per_item(const Plan &p, int batch, int n_items, int cu_count)
     if (n_items > kResidentWaves)
         return 0;  // more items than resident waves: kT tiles per wave (combine_tiles_kernel)
     const int slots = (p.n_slots + batch - 1) / batch;  // about the slots of one sequence
-    if (n_items < cu_count) {
+    if (n_items < cu_count || p.part_bytes == 4) {
         const int quads = (slots + 3) / 4;
         int waves = 1;
         while (waves < 16 && kUQ * waves < quads)

@@ -124,6 +124,13 @@ def run_case(lib, torch, n_h, n, splits, flags, k, spin_s):
                launch_us=round(us, 2), span_us=round(float((x[:, 10].max() - t0) * 0.01), 2),
                step_us=round(step_us, 3), step_cycles=round(float(np.median(cyc / steps))), clock_ghz=round(clk, 3),
                phases_med_min_max_us=phases)
+    if len(c):
+        def mmm(v):
+            v = (v - t0) * 0.01
+            return [round(float(np.median(v)), 2), round(float(v.min()), 2), round(float(v.max()), 2)]
+        rec.update(combine_waves=int(len(c)), combine_entry=mmm(c[:, 0]), combine_merged=mmm(c[:, 1]),
+                   combine_stored=mmm(c[:, 3]), gap_us=round(float((c[:, 0].min() - x[:, 3].max()) * 0.01), 2),
+                   combine_span_us=round(float((c[:, 3].max() - c[:, 0].min()) * 0.01), 2))
     del qs, cs, ws
     torch.cuda.empty_cache()
     return rec
@@ -288,6 +295,18 @@ def run_case_f32(lib, torch, n_h, n, splits, k, spin_s):
     b.record(stream)
     torch.cuda.synchronize()
     us = a.elapsed_time(b) * 1000.0 / k
+    # the combine's per-wave stamps of the second of two more back-to-back calls (its split stamps are the
+    # ones read below; the first call takes the GPU out of the idle that the stamp clearing leaves)
+    if lib.mla_timeline_clear_combine() != 0:
+        raise RuntimeError("mla_timeline_clear_combine failed")
+    launch()
+    launch()
+    torch.cuda.synchronize()
+    cb = np.zeros(16384 * 4, dtype=np.uint64)
+    if lib.mla_timeline_read_combine(cb.ctypes.data, cb.nbytes) != 0:
+        raise RuntimeError("mla_timeline_read_combine failed")
+    c = cb.reshape(-1, 4).astype(np.int64)
+    c = c[c[:, 0] > 0]
     buf = np.zeros(8192 * SLOTS, dtype=np.uint64)
     if lib.mla_timeline_read_f32(buf.ctypes.data, buf.nbytes) != 0:
         raise RuntimeError("mla_timeline_read_f32 failed")
@@ -314,6 +333,13 @@ def run_case_f32(lib, torch, n_h, n, splits, k, spin_s):
                o_work_a_cycles=round(float(np.median(x[:, 9] / steps))),
                o_work_b_cycles=round(float(np.median(x[:, 10] / steps))),
                phases_med_min_max_us=phases)
+    if len(c):
+        def mmm(v):
+            v = (v - t0) * 0.01
+            return [round(float(np.median(v)), 2), round(float(v.min()), 2), round(float(v.max()), 2)]
+        rec.update(combine_waves=int(len(c)), combine_entry=mmm(c[:, 0]), combine_merged=mmm(c[:, 1]),
+                   combine_stored=mmm(c[:, 3]), gap_us=round(float((c[:, 0].min() - x[:, 3].max()) * 0.01), 2),
+                   combine_span_us=round(float((c[:, 3].max() - c[:, 0].min()) * 0.01), 2))
     del qs, cs, ws
     torch.cuda.empty_cache()
     return rec
