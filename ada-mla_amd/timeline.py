@@ -124,13 +124,6 @@ def run_case(lib, torch, n_h, n, splits, flags, k, spin_s):
                launch_us=round(us, 2), span_us=round(float((x[:, 10].max() - t0) * 0.01), 2),
                step_us=round(step_us, 3), step_cycles=round(float(np.median(cyc / steps))), clock_ghz=round(clk, 3),
                phases_med_min_max_us=phases)
-    if len(c):
-        def mmm(v):
-            v = (v - t0) * 0.01
-            return [round(float(np.median(v)), 2), round(float(v.min()), 2), round(float(v.max()), 2)]
-        rec.update(combine_waves=int(len(c)), combine_entry=mmm(c[:, 0]), combine_merged=mmm(c[:, 1]),
-                   combine_stored=mmm(c[:, 3]), gap_us=round(float((c[:, 0].min() - x[:, 3].max()) * 0.01), 2),
-                   combine_span_us=round(float((c[:, 3].max() - c[:, 0].min()) * 0.01), 2))
     del qs, cs, ws
     torch.cuda.empty_cache()
     return rec
