@@ -122,12 +122,22 @@ constexpr double kDirectFixedUs = 7.0;
 // partial precision): a fixed cost per call (two launches, the prologue, the
 // partial store); the split kernel's block loop, one 32-token step per block
 // plus one at a step time that grows with the head tile (64: 1.5 us, 32:
-// 0.88 us, 16: 0.65 us with every CU busy), but no faster than streaming C
-// at ~6 TB/s; the partial round trip (written, then read by the combine)
-// at ~8 TB/s; and the combine's memory round trips. Head tiles that
+// 0.88 us, 16: 0.65 us with every CU busy), but no shorter than the HBM
+// time of every chunk in flight streaming its block at once
+// (kStreamBytesPerUs); the partial round trip (written, then read by the
+// combine) at ~8 TB/s; and the combine's memory round trips. Head tiles that
 // share a chunk but not an XCD (xcd_remap 0, which the planner no longer
 // produces) would re-read C from HBM; the model charges that as slower
 // steps.
+// The stream term is per block: a plan with fewer chunks than CUs streams C
+// with fewer CUs and is not HBM-bound until each block's share reaches the
+// step. Against a floor over the whole call (C at 6 TB/s), which made every
+// split count past the floor look alike and favoured the fewest partials,
+// it moved 13 of 156 plans (n_h 16 and 32, N >= 32768), all faster on one
+// box: n_h = 16, N = 65536 114 -> 137 splits 22.9 -> 20.3 us, N = 262144
+// 108 -> 139 splits 71.3 -> 58.5 us; n_h = 32, N = 65536 114 -> 128 splits
+// 23.1 -> 20.8 us, N = 262144 (16, 108) -> (32, 179) 71.2 -> 59.0 us.
+constexpr double kStreamBytesPerUs = 7.5e6;  // n_h = 16 streams C at 7.7 TB/s in the steady state
 double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, int cu_count, bool paged,
                    bool direct_ok)
 {
@@ -142,9 +152,16 @@ double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, in
     const double share = (p.n_head_tiles > 1 && !p.xcd_remap) ? 1.3 : 1.0;
     const double partial_bytes = (double)p.n_slots * num_heads * (kDV * p.part_bytes + 8);
     // the combine merges up to 128 slots of a tile per memory round trip
+    // (256 in quarter items: fewer items than CUs, or fp32 partials)
     const double slots_per_seq = std::ceil((double)p.n_slots / batch);
-    const double combine_trips = std::ceil(slots_per_seq / 128.0);
-    const double loop_us = std::max(rounds * steps * step_us * share, (double)total_tokens * kDK * 2 / 6.0e6);
+    const bool quarter = num_heads / 16 * (kDV / 16) * batch < cu_count || p.part_bytes == 4;
+    const double combine_trips = std::ceil(slots_per_seq / (quarter ? 256.0 : 128.0));
+    // a block takes its step, but no less than the HBM time of every chunk
+    // in flight streaming its block at once (the head tiles of a chunk read
+    // it from one L2)
+    const double chunks_live = std::min((double)wgs, (double)cu_count) / p.n_head_tiles;
+    const double block_us = std::max(step_us * share, chunks_live * p.block_tokens * kDK * 2 / kStreamBytesPerUs);
+    const double loop_us = rounds * steps * block_us;
     return 11.0 + loop_us + 0.25e-6 * partial_bytes + 1.0 * combine_trips;
 }
 

@@ -285,6 +285,23 @@ def test_head_tile_query():
     assert f(24, 100, 0, 0) == 0 and f(128, 0, 0, 0) == 0
 
 
+def test_few_head_long_sequences_stream_with_at_least_half_the_cus():
+    # With few heads C streams from HBM at the chip's rate only when enough
+    # chunks are in flight: the planner charges each block the HBM time of
+    # every chunk streaming at once, so at long N it keeps at least 128 of
+    # the 256 CUs busy (a floor over the whole call once chose 108-114
+    # chunks there, 12-18% slower on MI355X), and at N = 16384 stays at 128
+    # chunks, where more splits cost more in partials than they save.
+    lib = capi.load()
+    splits, tile = lib.mla_decode_split_num_splits, lib.mla_decode_split_head_tile
+    for n_h in (16, 32):
+        for n in (65536, 131072, 262144):
+            for flags in (0, capi.FLAG_FP32_PARTIALS):
+                workgroups = splits(n_h, n, 0, flags) * (n_h // tile(n_h, n, 0, flags))
+                assert 128 <= workgroups <= 256, (n_h, n, flags, workgroups)
+    assert splits(16, 16384, 0, 0) == 128
+
+
 def test_block_projection_argument_errors():
     lib = capi.load()
     for fn in ("mla_absorb_query_fp16", "mla_absorb_query_bf16"):
