@@ -510,6 +510,20 @@ def test_quarter_combine(n_h, n, splits, flags):
              f"n_h={n_h} N={n} splits={splits} flags={flags}")
 
 
+@pytest.mark.parametrize("n_h,n,flags", [(16, 65536, 0), (16, 65536 + 3, 4), (32, 65536, 0), (32, 131072 + 9, 4)])
+def test_few_heads_long_sequences_planner_plans(n_h, n, flags):
+    # the planner's own plans where few heads stream C: 137 chunks at
+    # n_h = 16 (a slot count that is not a multiple of 4 for the quarter
+    # combine), every CU busy at n_h = 32
+    lib = capi.load()
+    splits = lib.mla_decode_split_num_splits(n_h, n, 0, flags)
+    tile = lib.mla_decode_split_head_tile(n_h, n, 0, flags)
+    print(f"few heads n_h={n_h} N={n} flags={flags}: {splits} splits, {tile}-head tiles", flush=True)
+    assert splits * (n_h // tile) >= 128
+    q, c = synthetic.decode_inputs(n_h, n, seed=900 + n_h)
+    _check16(_fp16(q, c, flags=flags), O.closed_form(q, c), f"n_h={n_h} N={n} flags={flags}")
+
+
 @pytest.mark.parametrize("n_h,n,splits", [(16, 3000, 0), (16, 3000, 300), (32, 777, 5)])
 def test_quarter_combine_fp32(n_h, n, splits):
     print(f"quarter combine fp32 n_h={n_h} N={n} splits={splits}", flush=True)
