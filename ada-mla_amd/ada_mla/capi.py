@@ -25,6 +25,7 @@ STATUS_SCRATCH_EXCEEDED = 5
 NOALLOC_SCRATCH_BYTES = 32 << 20
 FLAG_SCALAR_TRANSPOSE = 1
 FLAG_FP32_PARTIALS = 4
+FLAG_FP8_CACHE = 16  # plan queries: the fp8-cache entries' plan
 FLAG_TWO_LAUNCHES = 8
 
 _vp, _i, _u, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint, ctypes.c_size_t

@@ -139,7 +139,7 @@ constexpr double kDirectFixedUs = 7.0;
 // 23.1 -> 20.8 us, N = 262144 (16, 108) -> (32, 179) 71.2 -> 59.0 us.
 constexpr double kStreamBytesPerUs = 7.5e6;  // n_h = 16 streams C at 7.7 TB/s in the steady state
 double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, int cu_count, bool paged,
-                   bool direct_ok)
+                   bool direct_ok, int c_bytes)
 {
     // one chunk of a single sequence: one launch, no partials, no combine
     if (direct_ok && p.n_chunks == 1)
@@ -158,9 +158,9 @@ double modelled_us(const Plan &p, int num_heads, int total_tokens, int batch, in
     const double combine_trips = std::ceil(slots_per_seq / (quarter ? 256.0 : 128.0));
     // a block takes its step, but no less than the HBM time of every chunk
     // in flight streaming its block at once (the head tiles of a chunk read
-    // it from one L2)
+    // it from one L2); c_bytes: bytes per cache element (1 for fp8)
     const double chunks_live = std::min((double)wgs, (double)cu_count) / p.n_head_tiles;
-    const double block_us = std::max(step_us * share, chunks_live * p.block_tokens * kDK * 2 / kStreamBytesPerUs);
+    const double block_us = std::max(step_us * share, chunks_live * p.block_tokens * kDK * c_bytes / kStreamBytesPerUs);
     const double loop_us = rounds * steps * block_us;
     return 11.0 + loop_us + 0.25e-6 * partial_bytes + 1.0 * combine_trips;
 }
@@ -211,42 +211,66 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch, bool se
     // fp16: the head tile (64, 32 or 16 heads per workgroup) and the split
     // count with the smallest modelled call time, at most one workgroup per
     // CU; a requested split count fixes the chunking and only the tile is
-    // chosen.
-    Plan best{};
-    double best_us = 0.0;
-    for (int ht : {64, 32, 16}) {
-        if (num_heads % ht != 0)
-            continue;
+    // chosen. Chosen splits leave chunks of at least two blocks once there
+    // are 32 blocks (a one-block chunk overlaps no load with compute: on
+    // MI355X 17 of 24 such plans ran 2-10% faster at two blocks, n_h = 16 ..
+    // 256, N = 1024 .. 4096; at N = 512 it was a wash).
+    // min_blocks(ht): the shortest chunk (in blocks) the search takes;
+    // c_bytes: bytes per cache element for the stream term.
+    auto search = [&](int c_bytes, auto min_blocks, double &best_us) {
+        Plan best{};
+        best_us = 0.0;
+        for (int ht : {64, 32, 16}) {
+            if (num_heads % ht != 0)
+                continue;
 #ifdef MLA_TIMELINE
-        // timeline build only (ada-mla_amd/timeline.py): MLA_TIMELINE_HEAD_TILE pins the tile
-        if (const char *e = std::getenv("MLA_TIMELINE_HEAD_TILE"); e && std::atoi(e) != ht)
-            continue;
+            // timeline build only (ada-mla_amd/timeline.py): MLA_TIMELINE_HEAD_TILE pins the tile
+            if (const char *e = std::getenv("MLA_TIMELINE_HEAD_TILE"); e && std::atoi(e) != ht)
+                continue;
 #endif
-        Plan c{};
-        c.head_tile = ht;
-        c.block_tokens = 32;
-        c.n_head_tiles = num_heads / ht;
-        c.part_bytes = f32_partials ? 4 : 2;
-        // with cu_seqlens the chunks split the virtual length (piece_cost_tokens)
-        // (plain token chunks if the virtual length would not fit an int)
-        c.seq_cost = seqlens ? piece_cost_tokens(ht) : 0;
-        if ((long long)total_tokens + (long long)c.seq_cost * batch > INT32_MAX / 2)
-            c.seq_cost = 0;
-        const int total_v = total_tokens + c.seq_cost * batch;
-        int w_lo = 1, w_hi = std::max(1, std::min(cu_count / c.n_head_tiles, ceil_div(total_v, c.block_tokens)));
-        if (num_splits > 0)
-            w_lo = w_hi = num_splits;
-        for (int w = w_lo; w <= w_hi; ++w) {
-            set_chunks(c, total_v, batch, w);
-            const double us = modelled_us(c, num_heads, total_tokens, batch, cu_count, paged,
-                                          !seqlens && cache != CacheKind::kPaged);
-            if (best_us == 0.0 || us < best_us) {
-                best = c;
-                best_us = us;
+            Plan c{};
+            c.head_tile = ht;
+            c.block_tokens = 32;
+            c.n_head_tiles = num_heads / ht;
+            c.part_bytes = f32_partials ? 4 : 2;
+            // with cu_seqlens the chunks split the virtual length (piece_cost_tokens)
+            // (plain token chunks if the virtual length would not fit an int)
+            c.seq_cost = seqlens ? piece_cost_tokens(ht) : 0;
+            if ((long long)total_tokens + (long long)c.seq_cost * batch > INT32_MAX / 2)
+                c.seq_cost = 0;
+            const int total_v = total_tokens + c.seq_cost * batch;
+            const int blocks = ceil_div(total_v, c.block_tokens);
+            int w_lo = 1, w_hi = std::max(1, std::min(cu_count / c.n_head_tiles, blocks / min_blocks(ht, blocks)));
+            if (num_splits > 0)
+                w_lo = w_hi = num_splits;
+            for (int w = w_lo; w <= w_hi; ++w) {
+                set_chunks(c, total_v, batch, w);
+                const double us = modelled_us(c, num_heads, total_tokens, batch, cu_count, paged,
+                                              !seqlens && cache != CacheKind::kPaged, c_bytes);
+                if (best_us == 0.0 || us < best_us) {
+                    best = c;
+                    best_us = us;
+                }
             }
         }
-    }
-    return best;
+        return best;
+    };
+    double us16 = 0.0;
+    const Plan p16 = search(2, [](int, int blocks) { return blocks >= 32 ? 2 : 1; }, us16);
+    if (cache != CacheKind::kF8 || num_splits > 0)
+        return p16;
+    // fp8 cache: its blocks stream half the bytes, so with few heads more
+    // chunks than the 16-bit plan's pay -- but only long ones (measured on
+    // MI355X: at 16-head tiles from four blocks per chunk, n_h = 16, N =
+    // 65536: 137 -> 256 chunks 17.0 -> 14.0 us; at 32-head tiles from
+    // sixteen, n_h = 32, N = 131072: 16 x 128 -> 32 x 256 27.1 -> 23.1 us;
+    // shorter chunks ran up to 18% slower). The 16-bit plan stays a
+    // candidate.
+    double us8 = 0.0;
+    const Plan p8 = search(1, [](int ht, int) { return ht == 16 ? 4 : 16; }, us8);
+    const double us16_as8 = modelled_us(p16, num_heads, total_tokens, batch, cu_count, paged,
+                                        !seqlens && cache != CacheKind::kPaged, 1);
+    return us8 < us16_as8 ? p8 : p16;
 }
 
 }  // namespace
@@ -315,6 +339,16 @@ size_t split_workspace_bytes(int num_heads, int total_tokens, int batch, bool se
 }
 
 bool heads_ok(int num_heads) { return num_heads > 0 && num_heads % 16 == 0 && num_heads <= 4096; }
+
+// The plan that the plan queries report: a single sequence's, on the current
+// device, for the fp8-cache entries with MLA_FLAG_FP8_CACHE (whose partials
+// are fp16), else for mla_decode_split_fp16_ex with these flags.
+Plan query_plan(int num_heads, int seq_length, int num_splits, unsigned flags)
+{
+    const bool f8 = (flags & MLA_FLAG_FP8_CACHE) != 0;
+    return make_plan(false, num_heads, seq_length, 1, false, num_splits, current_cu_count(),
+                     f8 ? CacheKind::kF8 : CacheKind::kPacked, !f8 && (flags & MLA_FLAG_FP32_PARTIALS) != 0);
+}
 
 constexpr int kPhaseSplit = 1;
 constexpr int kPhaseCombine = 2;
@@ -467,27 +501,24 @@ int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits, u
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    return mla::make_plan(false, num_heads, seq_length, 1, false, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
-                          (flags & MLA_FLAG_FP32_PARTIALS) != 0)
-        .n_chunks;
+    return mla::query_plan(num_heads, seq_length, num_splits, flags).n_chunks;
 }
 
 int mla_decode_split_head_tile(int num_heads, int seq_length, int num_splits, unsigned flags)
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    return mla::make_plan(false, num_heads, seq_length, 1, false, num_splits, mla::current_cu_count(), mla::CacheKind::kPacked,
-                          (flags & MLA_FLAG_FP32_PARTIALS) != 0)
-        .head_tile;
+    return mla::query_plan(num_heads, seq_length, num_splits, flags).head_tile;
 }
 
 int mla_decode_split_launches(int num_heads, int seq_length, int num_splits, unsigned flags)
 {
     if (!mla::heads_ok(num_heads) || seq_length < 1)
         return 0;
-    const mla::Plan p = mla::make_plan(false, num_heads, seq_length, 1, false, num_splits, mla::current_cu_count(),
-                                       mla::CacheKind::kPacked, (flags & MLA_FLAG_FP32_PARTIALS) != 0);
-    return mla::choose_merge(p, true, flags) == mla::kMergeCombine ? 2 : 1;
+    return mla::choose_merge(mla::query_plan(num_heads, seq_length, num_splits, flags), true, flags) ==
+                   mla::kMergeCombine
+               ? 2
+               : 1;
 }
 
 size_t mla_decode_split_workspace_size(int num_heads, int seq_length, int num_splits)

@@ -71,22 +71,30 @@ extern "C" {
  * combine (csrc/mla_decode_splitk_fwd.cuh:973-978). */
 #define MLA_FLAG_TWO_LAUNCHES 8u
 
+/* Plan queries only (mla_decode_split_num_splits, _head_tile, _launches):
+ * report the plan of the fp8-cache entry mla_decode_split_fp8 for these
+ * sizes. Its cache streams half the bytes of a 16-bit one, so with few heads
+ * and long sequences its plan can take more splits, or another head tile,
+ * than the 16-bit plan. The decode entry points ignore it. */
+#define MLA_FLAG_FP8_CACHE 16u
+
 int mla_abi_version(void);
 const char *mla_status_string(int status);
 /* hipError_t of the last failed HIP call on this thread (0 if none). */
 int mla_last_hip_error(void);
 
 /* Number of splits (partial results per head) that mla_decode_split_fp16_ex
- * uses for these arguments and flags on the current device; 0 for invalid
- * sizes.
+ * (with MLA_FLAG_FP8_CACHE: mla_decode_split_fp8) uses for these arguments
+ * and flags on the current device; 0 for invalid sizes.
  * Replaces the fixed `num_splits = 4` of mla_decode_split
  * (csrc/mla_api.cpp:97). */
 int mla_decode_split_num_splits(int num_heads, int seq_length, int num_splits,
                                 unsigned flags);
 
 /* Heads per workgroup (16, 32 or 64) of the plan that
- * mla_decode_split_fp16_ex uses for these arguments and flags on the current
- * device, and mla_decode_split_fp8 for the same sizes; 0 for invalid sizes.
+ * mla_decode_split_fp16_ex (with MLA_FLAG_FP8_CACHE: mla_decode_split_fp8)
+ * uses for these arguments and flags on the current device; 0 for invalid
+ * sizes.
  * With an fp8 cache, tiles of 32 or 64 heads run the first product on fp8
  * MFMAs (Q* split in two fp8 parts), tiles of 16 convert C to fp16. No
  * counterpart in the reference. */
@@ -94,8 +102,8 @@ int mla_decode_split_head_tile(int num_heads, int seq_length, int num_splits,
                                unsigned flags);
 
 /* Kernel launches (1 or 2, see MLA_FLAG_TWO_LAUNCHES) that
- * mla_decode_split_fp16_ex makes for these arguments and flags on the
- * current device; 0 for invalid sizes. No counterpart in the reference, whose
+ * mla_decode_split_fp16_ex (with MLA_FLAG_FP8_CACHE: mla_decode_split_fp8)
+ * makes for these arguments and flags on the current device; 0 for invalid sizes. No counterpart in the reference, whose
  * launcher always makes two (csrc/mla_decode_splitk_fwd.cuh:973-978). */
 int mla_decode_split_launches(int num_heads, int seq_length, int num_splits,
                               unsigned flags);

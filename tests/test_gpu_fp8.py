@@ -83,7 +83,7 @@ def test_fp8_query_dynamic_range(n_h, q_scale, c_scale):
     # a 64-head tile (128 heads, N = 65536) and a 32-head tile (32 heads,
     # 200 splits of N = 20000).
     n, splits = (65536, 0) if n_h == 128 else (20000, 200)
-    assert capi.load().mla_decode_split_head_tile(n_h, n, splits, 0) == (64 if n_h == 128 else 32)
+    assert capi.load().mla_decode_split_head_tile(n_h, n, splits, capi.FLAG_FP8_CACHE) == (64 if n_h == 128 else 32)
     print(f"fp8 dynamic range n_h={n_h} q_scale={q_scale}", flush=True)
     q = synthetic.normal((n_h, 576), 77, np.float32)
     q = q * (2.0 ** np.linspace(-2.0, 2.0, n_h))[:, None] * q_scale
@@ -108,7 +108,7 @@ def test_fp8_query_near_fp16_max(n_h):
     # 65504, 64000, 63488, 40000 and 32768 (and, for contrast, 30000), with a
     # cache scale that keeps the logits of order one.
     n, splits = (65536, 0) if n_h == 128 else (20000, 200)
-    assert capi.load().mla_decode_split_head_tile(n_h, n, splits, 0) == (64 if n_h == 128 else 32)
+    assert capi.load().mla_decode_split_head_tile(n_h, n, splits, capi.FLAG_FP8_CACHE) == (64 if n_h == 128 else 32)
     print(f"fp8 query near fp16 max n_h={n_h}", flush=True)
     q = synthetic.normal((n_h, 576), 91, np.float32)
     tops = np.array([65504.0, 64000.0, 63488.0, 40000.0, 32768.0, 30000.0])
@@ -147,7 +147,7 @@ def test_fp8_batched_with_empty():
 def test_fp8_several_head_tiles(n_h, n, tile):
     # fp8 first product on three head tiles of 32 or 64 heads per chunk
     # (the Q* split of each tile in its own workgroups)
-    assert capi.load().mla_decode_split_head_tile(n_h, n, 0, 0) == tile
+    assert capi.load().mla_decode_split_head_tile(n_h, n, 0, capi.FLAG_FP8_CACHE) == tile
     print(f"fp8 n_h={n_h} N={n} head tile {tile}", flush=True)
     q, c8, cd = _fp8_inputs(n_h, n, seed=90 + n_h, scale=0.5)
     out = capi.decode_split_fp8(torch.from_numpy(q).cuda(), c8.cuda(), 0.5)
