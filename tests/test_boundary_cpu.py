@@ -290,8 +290,9 @@ def test_few_head_long_sequences_stream_with_at_least_half_the_cus():
     # chunks are in flight: the planner charges each block the HBM time of
     # every chunk streaming at once, so at long N it keeps at least 128 of
     # the 256 CUs busy (a floor over the whole call once chose 108-114
-    # chunks there, 12-18% slower on MI355X), and at N = 16384 stays at 128
-    # chunks, where more splits cost more in partials than they save.
+    # chunks there, 12-18% slower on MI355X; once its blocks wait on HBM a plan
+    # takes every CU), and at N = 16384 stays at 128 chunks, where more splits
+    # cost more in partials than they save.
     lib = capi.load()
     splits, tile = lib.mla_decode_split_num_splits, lib.mla_decode_split_head_tile
     for n_h in (16, 32):
@@ -304,14 +305,14 @@ def test_few_head_long_sequences_stream_with_at_least_half_the_cus():
 
 def test_fp8_cache_plan_query():
     # MLA_FLAG_FP8_CACHE asks the plan queries for the fp8-cache entries'
-    # plan: their cache streams half the bytes, so with few heads C does not
-    # bind the block time and every CU takes a chunk (n_h = 16, N = 65536:
-    # 256 chunks, 18% faster on MI355X than the 16-bit plan's 137); with 128
-    # heads the two plans are the same
+    # plan: their cache streams half the bytes, so with few heads more chunks
+    # pay before C binds the block time (n_h = 16, N = 32768: 256 chunks, 5%
+    # faster on MI355X than the 16-bit plan's 128); with 128 heads the two
+    # plans are the same
     lib = capi.load()
     splits, tile = lib.mla_decode_split_num_splits, lib.mla_decode_split_head_tile
     f8 = capi.FLAG_FP8_CACHE
-    assert splits(16, 65536, 0, f8) == 256 and splits(16, 65536, 0, 0) == 137
+    assert splits(16, 32768, 0, f8) == 256 and splits(16, 32768, 0, 0) == 128
     for n in (4096, 65536):
         assert (splits(128, n, 0, f8), tile(128, n, 0, f8)) == (splits(128, n, 0, 0), tile(128, n, 0, 0))
     # the fp8 entries keep fp16 partials: the fp32-partials flag does not change their plan

@@ -512,9 +512,9 @@ def test_quarter_combine(n_h, n, splits, flags):
 
 @pytest.mark.parametrize("n_h,n,flags", [(16, 65536, 0), (16, 65536 + 3, 4), (32, 65536, 0), (32, 131072 + 9, 4)])
 def test_few_heads_long_sequences_planner_plans(n_h, n, flags):
-    # the planner's own plans where few heads stream C: 137 chunks at
-    # n_h = 16 (a slot count that is not a multiple of 4 for the quarter
-    # combine), every CU busy at n_h = 32
+    # the planner's own plans where few heads stream C: every CU busy (256
+    # chunks at n_h = 16; 128 chunks of two 16-head tiles or 256 of one
+    # 32-head tile at n_h = 32)
     lib = capi.load()
     splits = lib.mla_decode_split_num_splits(n_h, n, 0, flags)
     tile = lib.mla_decode_split_head_tile(n_h, n, 0, flags)
