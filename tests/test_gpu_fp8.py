@@ -143,6 +143,21 @@ def test_fp8_batched_with_empty():
             _check(got[b], ref[b], f"seq {b}")
 
 
+@pytest.mark.parametrize("n_h,n,tile", [(16, 65536 + 5, 16), (32, 131072, 32)])
+def test_fp8_few_heads_long_sequences(n_h, n, tile):
+    # the fp8 plans of their own: with few heads about every CU takes a chunk
+    # (228 chunks of 16 heads at N = 65541, where a chunk rounds up to 9
+    # blocks; 256 of one 32-head tile, whose first product runs on fp8 MFMAs)
+    lib = capi.load()
+    assert lib.mla_decode_split_num_splits(n_h, n, 0, capi.FLAG_FP8_CACHE) > 200
+    assert lib.mla_decode_split_head_tile(n_h, n, 0, capi.FLAG_FP8_CACHE) == tile
+    print(f"fp8 few heads n_h={n_h} N={n}", flush=True)
+    q, c8, cd = _fp8_inputs(n_h, n, seed=60 + n_h, scale=0.5)
+    out = capi.decode_split_fp8(torch.from_numpy(q).cuda(), c8.cuda(), 0.5)
+    torch.cuda.synchronize()
+    _check(out.double().cpu().numpy(), O.closed_form(q, cd), f"n_h={n_h} N={n}")
+
+
 @pytest.mark.parametrize("n_h,n,tile", [(96, 20000, 32), (192, 40000, 64), (64, 30000, 32)])
 def test_fp8_several_head_tiles(n_h, n, tile):
     # fp8 first product on three head tiles of 32 or 64 heads per chunk

@@ -292,6 +292,18 @@ def test_config5_batched():
         _check16(got[b], O.closed_form(q[b], c[lo:hi]), f"config 5 seq {b} N={hi - lo}")
 
 
+def test_config5_lengths_at_16_heads():
+    # config 5's lengths with 16 heads (a tensor-parallel share of 128): the
+    # planner's plan is stream-bound and takes every CU, 256 chunks over 32
+    # sequences, so many chunks hold two or three pieces
+    seqlens = synthetic.batched_seqlens(32, seed=42)
+    q, c, cu = synthetic.batched_inputs(16, seqlens, seed=43)
+    got = _batched(q, c, cu)
+    ref = O.closed_form_batched(q, c, cu)
+    for b in range(32):
+        _check16(got[b], ref[b], f"16 heads, config 5 seq {b} N={cu[b + 1] - cu[b]}")
+
+
 @pytest.mark.parametrize("n_h,batch,splits", [(128, 24, 0), (128, 24, 7), (128, 24, 200), (16, 160, 0), (48, 48, 13)])
 def test_batched_many_items_with_empty(n_h, batch, splits):
     # more (16 x 16 tile, sequence) items than the combine keeps resident
