@@ -384,11 +384,16 @@ int choose_merge(const Plan &p, bool single16, unsigned flags)
 // N = 65536 with fp32 partials (256) 37.4 -> 38.3 us, batched (512) 94.2 -> 93.5.
 // The quarter-tile combine (fewer (tile, sequence) items than CUs) also
 // reads plain stored partials faster: n_h = 16, 128 splits (128 combine
-// workgroups of 8 waves) 14.07 -> 13.82 us.
+// workgroups of 8 waves) 14.07 -> 13.82 us. So does the tile-group combine
+// of large batches (more items than resident waves), by a little: medians of
+// three calls, one box, batched 94.25 -> 93.96 us, paged 97.47 -> 96.87,
+// fp8 batched 82.25 -> 81.63, MLA block step 138.83 -> 138.11.
 int choose_part_plain(const Plan &p, int batch, int num_heads, int cu_count)
 {
     const int items = num_heads / 16 * (kDV / 16) * batch;
-    return (items < cu_count || 4 * combine_workgroups(p, batch, num_heads, cu_count) < cu_count) ? 1 : 0;
+    const bool tile_groups = combine_waves_per_item(p, batch, items, cu_count) == 0;
+    return (items < cu_count || tile_groups || 4 * combine_workgroups(p, batch, num_heads, cu_count) < cu_count) ? 1
+                                                                                                               : 0;
 }
 
 // Shared body of every entry point; `phases` selects the split kernel, the

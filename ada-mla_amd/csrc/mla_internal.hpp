@@ -117,6 +117,10 @@ hipError_t launch_splitkv_fp32(const Problem &pb, const Plan &p,
 // on the fp32 path.
 // Workgroups of the combine launch for plan p (batch sequences, num_heads).
 int combine_workgroups(const Plan &p, int batch, int num_heads, int cu_count);
+// The combine's form for n_items (16 x 16 tile, sequence) items: W > 0 waves
+// per item, 0 for tile groups (more items than resident waves), -W for
+// quarter items.
+int combine_waves_per_item(const Plan &p, int batch, int n_items, int cu_count);
 
 hipError_t launch_combine(const Problem &pb, const Plan &p, const Partials &w,
                           hipStream_t s);
