@@ -213,8 +213,9 @@ Plan compute_plan(bool fp32, int num_heads, int total_tokens, int batch, bool se
     // CU; a requested split count fixes the chunking and only the tile is
     // chosen. Chosen splits leave chunks of at least two blocks once there
     // are 32 blocks (a one-block chunk overlaps no load with compute: on
-    // MI355X 17 of 24 such plans ran 2-10% faster at two blocks, n_h = 16 ..
-    // 256, N = 1024 .. 4096; at N = 512 it was a wash).
+    // MI355X the 19 plans this moved, n_h = 16 .. 128, N = 1024 .. 4096, ran
+    // x0.962 by geomean, 13 faster by more than 2%, one 2.7% slower; at
+    // N = 512 it was a wash).
     // min_blocks(ht): the shortest chunk (in blocks) the search takes;
     // c_bytes: bytes per cache element for the stream term.
     auto search = [&](int c_bytes, auto min_blocks, double &best_us) {
