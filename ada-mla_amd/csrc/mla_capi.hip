@@ -51,6 +51,9 @@ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // blocks; with one, the fp32 partial write-back about equals the C bytes the
 // split reads). Measured at 128 heads, N = 1024: 16.7 us per call with
 // 32-token splits (256 workgroups), 18.4 us with 64-token splits (128).
+// Re-measured on the current kernel (one box, us per call, 16 / 20 / 24 /
+// 28 / 32 splits): N = 1024 13.94 / 13.92 / 13.55 / 13.55 / 13.53; N = 2048
+// (16, 24, 32) 20.5 / 18.6 / 16.9; N = 4096 (24, 28, 32) 26.6 / 25.4 / 23.3.
 constexpr int kMinSplitTokensF32 = 32;
 
 // fp32 path: 32-head workgroups once their chunks hold this many tokens (12
