@@ -94,3 +94,37 @@ def test_offsets_past_2_31_elements(cache):
         _check(single.double().cpu().numpy(), want, f"{cache} single sequence {i}")
     del c
     torch.cuda.empty_cache()
+
+
+def test_paged_pages_past_2_31_elements():
+    """The paged cache: sequence 0 on the last 47 physical pages (all past
+    2^31 elements) in reverse order, sequence 1 alternating between low pages
+    and pages past the offset; block-table columns past a sequence's pages
+    hold ids out of range."""
+    dev = torch.device("cuda:0")
+    page, num_pages = 64, 60_000  # 3.84 M tokens of fp16: 4.1 GiB
+    lens = [3000, 1000]
+    n_pg = [(n + page - 1) // page for n in lens]
+    pages = [[num_pages - 1 - j for j in range(n_pg[0])],
+             [j if j % 2 == 0 else num_pages - 200 - j for j in range(n_pg[1])]]
+    assert min(pages[0]) * page * 576 > 2**31 and max(pages[1]) * page * 576 > 2**31
+    print(f"large paged cache: {num_pages} pages of {page}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(12)
+    kv = torch.zeros(num_pages, page, 576, device=dev, dtype=torch.float16)
+    for pg in pages:
+        idx = torch.tensor(pg, device=dev)
+        kv[idx] = torch.randn(len(pg), page, 576, device=dev, generator=g).half()
+    bt = torch.full((2, max(n_pg)), num_pages + 12345, dtype=torch.int32)
+    for b, pg in enumerate(pages):
+        bt[b, :len(pg)] = torch.tensor(pg, dtype=torch.int32)
+    cu = torch.tensor([0, lens[0], lens[0] + lens[1]], dtype=torch.int32, device=dev)
+    q = torch.randn(2, N_H, 576, device=dev, generator=g).half()
+    out = capi.decode_paged(q, kv, bt.to(dev), cu, sum(lens))
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    for b, pg in enumerate(pages):
+        rows = kv[torch.tensor(pg, device=dev)].reshape(-1, 576)[:lens[b]].double().cpu().numpy()
+        want = O.closed_form(q[b].double().cpu().numpy(), rows)
+        _check(got[b], want, f"paged sequence {b} ({lens[b]} tokens)")
+    del kv
+    torch.cuda.empty_cache()
