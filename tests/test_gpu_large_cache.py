@@ -128,3 +128,29 @@ def test_paged_pages_past_2_31_elements():
         _check(got[b], want, f"paged sequence {b} ({lens[b]} tokens)")
     del kv
     torch.cuda.empty_cache()
+
+
+def test_fp32_offsets_past_2_31_elements():
+    """The fp32 path (mla_decode_fused_fp32) on the same construction: a
+    3.8 M-token fp32 cache, and a sequence that starts past 2^31 elements;
+    atol = rtol = 1e-4."""
+    dev = torch.device("cuda:0")
+    total = N_BIG + N_SMALL
+    print(f"large cache: fp32, {total} tokens, {total * 576 * 4 / 2**30:.2f} GiB", flush=True)
+    g = torch.Generator(device=dev).manual_seed(13)
+    c = torch.zeros(total, 576, device=dev, dtype=torch.float32)
+    c[:EDGE] = HEAD_SCALE * torch.randn(EDGE, 576, device=dev, generator=g)
+    c[N_BIG - EDGE:N_BIG] = TAIL_SCALE * torch.randn(EDGE, 576, device=dev, generator=g)
+    c[N_BIG:] = torch.randn(N_SMALL, 576, device=dev, generator=g)
+    q = torch.randn(2, N_H, 576, device=dev, generator=g)
+    rows = torch.cat([c[:EDGE], c[N_BIG - EDGE:N_BIG]]).double().cpu().numpy()
+    q_np = q.double().cpu().numpy()
+    wants = [_closed_form_sparse(q_np[0], rows, N_BIG - 2 * EDGE),
+             O.closed_form(q_np[1], c[N_BIG:].double().cpu().numpy())]
+    for i, part in enumerate([c[:N_BIG], c[N_BIG:]]):
+        got = capi.decode_fused_fp32(q[i].contiguous(), part)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(got.double().cpu().numpy(), wants[i], atol=1e-4, rtol=1e-4,
+                                   err_msg=f"fp32 sequence {i}")
+    del c
+    torch.cuda.empty_cache()
