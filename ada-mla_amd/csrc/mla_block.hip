@@ -192,11 +192,14 @@ __global__ __launch_bounds__(64) void value_proj_kernel(const E *__restrict__ o_
 //    on 256 CUs would leave 96 idle). A unit that one workgroup covers whole
 //    is stored directly; the pieces of a unit split between workgroups (at
 //    most a first and a last one per workgroup) are stored as fp32 partial
-//    tiles (nontemporal: read once) that reduce_units_kernel adds in a fixed
-//    order. (Adding them up in the kernel instead, by the last workgroup to
-//    finish a piece of the unit on agent-scope completion counters, measured
-//    slower: 40.3 us against 32.4 + 4.8 us for the two kernels, from the
-//    release / acquire cache maintenance.)
+//    tiles that reduce_units_kernel adds in a fixed order. Plain stores and
+//    loads: against nontemporal ones the call (value projection, W_O and the
+//    reduce, cold weights) read 41.2-41.4 against 41.6 us at B = 32, d_model
+//    5120, and 0.4-1.9% less at four other shapes. (Adding the pieces up in
+//    the kernel instead, by the last workgroup to finish a piece of the unit
+//    on agent-scope completion counters, measured slower: 40.3 us against
+//    32.4 + 4.8 us for the two kernels, from the release / acquire cache
+//    maintenance.)
 //  * Within a workgroup the chunks run through one kStages-deep LDS ring
 //    with no break at unit boundaries: 64 rows of W_O and 32 rows of x per
 //    stage, filled by direct global->LDS loads of 512 contiguous bytes of two
@@ -338,7 +341,7 @@ __global__ __launch_bounds__(256) void out_proj_kernel(const E *__restrict__ x, 
             const int b = sp.b0 + bl, n = sp.n0 + cl;
             if (!whole) {
                 // every row and column of the tile, so the sums stay in bounds
-                __builtin_nontemporal_store(v, (floatx4 *)(part + (size_t)slot * kPartTile + bl * kCols + cl));
+                *(floatx4 *)(part + (size_t)slot * kPartTile + bl * kCols + cl) = v;
             } else if (b < batch) {
                 E *o = out + (size_t)b * N + n;
                 if (n + 3 < N && (N & 3) == 0) {
@@ -383,7 +386,7 @@ __global__ __launch_bounds__(256) void reduce_units_kernel(const float *__restri
         for (int i = 0; i < 8; ++i) {
             const int g = g0 + i;
             const int slot = 2 * g + (u == g * geo.per_wg / geo.chunks ? 0 : 1);
-            p[i] = g <= g_hi ? __builtin_nontemporal_load((const floatx4 *)(tile0 + (size_t)slot * kPartTile))
+            p[i] = g <= g_hi ? *(const floatx4 *)(tile0 + (size_t)slot * kPartTile)
                              : floatx4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
